@@ -1,0 +1,111 @@
+/*
+ * paged_kv.h — C ABI of the MI355X (gfx950) paged-KV hot path.
+ *
+ * Every entry point takes plain device pointers, element strides and sizes, a dtype
+ * code and a hipStream_t passed as void*. None allocates device memory, copies
+ * synchronously or synchronises, so every call can be recorded into a hipGraph.
+ * Buffers are owned by the caller. Calls return 0 on success, a negative PKV_E_* code
+ * when the arguments are rejected before anything is launched, or a positive
+ * hipError_t when the launch itself fails.
+ *
+ * Pool layout (one layer): [num_slots, num_kv_heads, head_dim], slot = block * block_size
+ * + offset, exactly the layout of PagedKVCache.k[layer] in
+ * engine/runtime/paged_cache.py:32-35 of the reference.
+ */
+#ifndef PAGED_KV_H
+#define PAGED_KV_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype codes */
+#define PKV_F32 0
+#define PKV_F16 1
+#define PKV_BF16 2
+
+/* validation errors (negative) */
+#define PKV_E_DTYPE (-1)     /* unsupported dtype or dtype combination */
+#define PKV_E_SHAPE (-2)     /* unsupported head_dim / group size / block size / sizes */
+#define PKV_E_ALIGN (-3)     /* pointer or stride not aligned for 16-byte vector access */
+#define PKV_E_WORKSPACE (-4) /* split-K workspace missing or too small */
+#define PKV_E_NULL (-5)      /* required pointer is NULL */
+
+/* ABI version, bumped on any signature change. */
+int pkv_abi_version(void);
+
+/* Human-readable text for a status code returned by any entry point. */
+const char* pkv_status_string(int status);
+
+/*
+ * KV append: k_pool[slots[i]] = convert(k_new[i]), v_pool[slots[i]] = convert(v_new[i]).
+ * Replaces PagedKVCache.write (reference engine/runtime/paged_cache.py:42-45), i.e.
+ * two Tensor.index_copy_(0, slots, x.to(pool dtype)) calls. Conversions round to nearest
+ * even (float -> bf16 maps NaN to 0x7FC0, as torch does). Rows whose slot is outside
+ * [0, num_slots) are skipped (no write). Duplicate slots: one of the rows wins.
+ * k_new / v_new: [n_tokens, num_kv_heads, head_dim] with unit stride in head_dim.
+ */
+int pkv_kv_append(void* k_pool, void* v_pool, int pool_dtype, int64_t pool_stride_slot,
+                  int64_t pool_stride_head, int64_t num_slots, const void* k_new,
+                  int64_t k_stride_tok, int64_t k_stride_head, const void* v_new,
+                  int64_t v_stride_tok, int64_t v_stride_head, int new_dtype,
+                  const int64_t* slots, int64_t n_tokens, int32_t num_kv_heads,
+                  int32_t head_dim, void* stream);
+
+/*
+ * Block copy for prefix-cache copy-on-write. No counterpart exists in the reference
+ * (its prefix cache only shares full, never-written blocks; see
+ * engine/runtime/block_manager.py:130-150); this is the operation a block manager calls
+ * before appending into a shared block. For every layer l < num_layers and pair i:
+ *   pool[l, dst_i*block_size : (dst_i+1)*block_size] = pool[l, src_i*block_size : ...]
+ * for both pools. block_mapping is a device int64 array [n_pairs, 2] of (src, dst).
+ * block_bytes = block_size * num_kv_heads * head_dim * element size (a block is
+ * contiguous inside one layer). Pairs with src or dst outside [0, num_blocks) are
+ * skipped. A dst that is also some pair's src gives an unspecified result.
+ */
+int pkv_copy_blocks(void* k_pool, void* v_pool, int64_t layer_stride_bytes,
+                    int32_t num_layers, int64_t block_bytes, int64_t num_blocks,
+                    const int64_t* block_mapping, int64_t n_pairs, void* stream);
+
+/*
+ * Number of context splits the decode kernel uses for a block table of max_blocks
+ * columns when each split covers split_blocks blocks (1 <= split_blocks <= 64).
+ */
+int32_t pkv_decode_num_splits(int32_t max_blocks, int32_t split_blocks);
+
+/* Workspace bytes pkv_paged_decode needs (0 when num_splits == 1). */
+int64_t pkv_decode_workspace_bytes(int32_t batch, int32_t num_heads, int32_t head_dim,
+                                   int32_t num_splits);
+
+/*
+ * Paged decode attention (GQA, split-K flash decoding + combine). Replaces
+ * paged_decode_attention and its Triton kernels (reference
+ * engine/kernels/paged_attention.py:44-179). For sequence b and query head h:
+ *   n    = clamp(context_lens[b], 0, max_blocks * block_size)
+ *   slot = block_tables[b, p / block_size] * block_size + p % block_size, p < n
+ *   out[b, h] = softmax_p(scale * q[b,h] . k[slot_p, h / G]) @ v[slot_p, h / G]
+ * with G = num_heads / num_kv_heads, fp32 softmax and accumulation. n == 0 gives 0.
+ * q: [batch, num_heads, head_dim] in kv_dtype; out: same shape, kv_dtype or PKV_F32.
+ * k_cache / v_cache share strides (stride_slot, stride_head, 1).
+ * block_tables: int32 [batch, >= max_blocks] with row stride table_stride.
+ * head_dim in {16, 32, 64, 128, 256}; split_blocks in [1, 64]. When
+ * pkv_decode_num_splits(max_blocks, split_blocks) > 1 the caller passes a workspace of
+ * at least pkv_decode_workspace_bytes(...) bytes (any contents).
+ */
+int pkv_paged_decode(void* out, int out_dtype, int64_t out_stride_b, int64_t out_stride_h,
+                     const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                     const void* k_cache, const void* v_cache, int kv_dtype,
+                     int64_t kv_stride_slot, int64_t kv_stride_head, int64_t num_slots,
+                     const int32_t* block_tables, int64_t table_stride, int32_t max_blocks,
+                     const int32_t* context_lens, int32_t batch, int32_t num_heads,
+                     int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                     float scale, int32_t split_blocks, void* workspace,
+                     int64_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PAGED_KV_H */

@@ -1,0 +1,176 @@
+"""Paged decode attention on MI355X (gfx950), same call signatures as the reference's
+``engine/kernels/paged_attention.py``.
+
+``paged_decode_attention`` runs two hand-written HIP kernels through the C ABI of
+lib/libpaged_kv.so:
+
+1. a split-K pass: one wave per (sequence, KV head, context split) streams the split's
+   K/V rows straight from the paged pool through the block table with 16-byte loads,
+   computes the scores of every query head sharing that KV head (GQA: each K/V row is
+   read once for the whole group), and keeps an fp32 online softmax. A sequence whose
+   context fits one split writes its output directly.
+2. a combine pass that merges the splits of longer contexts with log-sum-exp weights.
+
+The number of splits depends only on the block-table width (a static shape), never on
+the context lengths (device data), so one hipGraph capture serves every length, as the
+reference's CUDA-graph decode requires (reference engine/runtime/cuda_graphs.py:10-11).
+Nothing here allocates outside torch's caching allocator or synchronises.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from engine.kernels import _native
+
+# The reference exposes HAS_TRITON for engine/kernels/fused.py (reference
+# engine/kernels/paged_attention.py:29-35). This build has no Triton anywhere.
+HAS_TRITON = False
+
+SUPPORTED_HEAD_DIMS = (16, 32, 64, 128, 256)
+_WAVES_TARGET = 2048  # ~8 waves per CU on 256 CUs
+_SPLIT_TOKENS_MAX = 512
+_SPLIT_TOKENS_MIN = 64
+
+
+def available(device: torch.device) -> bool:
+    """True when ``device`` is a GPU and the HIP library loads (reference :38-39)."""
+    if device.type != "cuda":
+        return False
+    try:
+        _native.lib()
+    except (RuntimeError, OSError):
+        return False
+    return True
+
+
+def use_gqa_kernel(dtype: torch.dtype, groups: int, head_dim: int) -> bool:
+    """Reference :182-189. Here one kernel serves every dtype and group size (query heads
+    sharing a KV head are always read together), so this only reports whether the
+    reference would have picked its grouped kernel for these arguments."""
+    return (
+        dtype in (torch.bfloat16, torch.float16)
+        and groups <= 16
+        and head_dim >= 16
+        and head_dim & (head_dim - 1) == 0
+    )
+
+
+def decode_split_blocks(batch: int, num_kv_heads: int, groups: int, max_blocks: int,
+                        block_size: int) -> int:  # fmt: skip
+    """Blocks per context split. Static shapes only (graph-safe). Splits are at most
+    512 tokens; they shrink (down to 64 tokens) until the grid offers ~2048 waves."""
+    heads_per_wave = groups if groups <= 4 else next(
+        (c for c in (4, 3, 2) if groups % c == 0), 1
+    )  # fmt: skip
+    tasks = batch * num_kv_heads * (groups // heads_per_wave)
+    hi = max(1, min(64, _SPLIT_TOKENS_MAX // block_size))
+    lo = max(1, min(hi, _SPLIT_TOKENS_MIN // block_size))
+    sb = hi
+    while sb > lo and tasks * -(-max(max_blocks, 1) // sb) < _WAVES_TARGET:
+        sb //= 2
+    return max(sb, lo)
+
+
+def paged_decode_attention(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    context_lens: torch.Tensor,
+    block_size: int,
+    block_n: int = 64,
+    *,
+    out: torch.Tensor | None = None,
+    split_blocks: int | None = None,
+) -> torch.Tensor:
+    """q: [B, nh, hd]; k_cache, v_cache: [num_slots, nkv, hd] (one layer);
+    block_tables: [B, max_blocks] int32; context_lens: [B] int32 -> [B, nh, hd].
+
+    Reference: engine/kernels/paged_attention.py:140-179. ``block_n`` (the reference's
+    Triton tile) is accepted and ignored. Extensions: ``out`` receives the result in
+    place ([B, nh, hd], q.dtype or float32 for the unrounded fp32 result) and
+    ``split_blocks`` overrides the context split size (1..64 blocks).
+    """
+    del block_n
+    what = "paged_decode_attention"
+    dev = _native.require_gpu(what, q, k_cache, v_cache, block_tables, context_lens)
+    if q.dim() != 3 or k_cache.dim() != 3 or v_cache.dim() != 3:
+        raise ValueError(f"{what}: q, k_cache, v_cache must be 3-D")
+    b, nh, hd = q.shape
+    nkv = k_cache.shape[1]
+    if v_cache.shape != k_cache.shape or k_cache.shape[2] != hd:
+        raise ValueError(f"{what}: cache shapes {tuple(k_cache.shape)}, "
+                         f"{tuple(v_cache.shape)} do not match q {tuple(q.shape)}")  # fmt: skip
+    if nh % nkv:
+        raise ValueError(f"{what}: {nh} query heads not a multiple of {nkv} KV heads")
+    if hd not in SUPPORTED_HEAD_DIMS:
+        raise ValueError(f"{what}: head_dim {hd} not in {SUPPORTED_HEAD_DIMS}")
+    if q.dtype != k_cache.dtype or v_cache.dtype != k_cache.dtype:
+        raise TypeError(f"{what}: q {q.dtype} and caches {k_cache.dtype}/{v_cache.dtype} "
+                        "must share one dtype")  # fmt: skip
+    if k_cache.stride() != v_cache.stride() or k_cache.stride(2) != 1:
+        raise ValueError(f"{what}: k_cache and v_cache need equal strides, unit in head_dim")
+    if block_tables.dtype != torch.int32 or context_lens.dtype != torch.int32:
+        raise TypeError(f"{what}: block_tables and context_lens must be int32")
+    if block_tables.dim() != 2 or block_tables.shape[0] != b or block_tables.stride(1) != 1:
+        raise ValueError(f"{what}: block_tables must be [B, max_blocks] with unit column stride")
+    if context_lens.shape != (b,) or not context_lens.is_contiguous():
+        raise ValueError(f"{what}: context_lens must be a contiguous [B] tensor")
+    if block_size <= 0:
+        raise ValueError(f"{what}: block_size must be positive")
+    kv_code = _native.dtype_code(k_cache.dtype, what)
+
+    q = q.contiguous()
+    if out is None:
+        out = torch.empty_like(q)
+    elif out.shape != q.shape or out.dtype not in (q.dtype, torch.float32) or \
+            out.stride(2) != 1 or out.device != dev:  # fmt: skip
+        raise ValueError(f"{what}: out must be [B, nh, hd] of {q.dtype} or float32 on {dev}")
+    if b == 0:
+        return out
+
+    max_blocks = block_tables.shape[1]
+    groups = nh // nkv
+    if split_blocks is None:
+        split_blocks = decode_split_blocks(b, nkv, groups, max_blocks, block_size)
+    lib = _native.lib()
+    splits = lib.pkv_decode_num_splits(max_blocks, split_blocks)
+    ws_bytes = lib.pkv_decode_workspace_bytes(b, nh, hd, splits)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
+    status = lib.pkv_paged_decode(
+        out.data_ptr(), _native.dtype_code(out.dtype, what), out.stride(0), out.stride(1),
+        q.data_ptr(), q.stride(0), q.stride(1),
+        k_cache.data_ptr(), v_cache.data_ptr(), kv_code,
+        k_cache.stride(0), k_cache.stride(1), k_cache.shape[0],
+        block_tables.data_ptr(), block_tables.stride(0), max_blocks,
+        context_lens.data_ptr(), b, nh, nkv, hd, block_size,
+        hd**-0.5, split_blocks, ws.data_ptr() if ws is not None else None, ws_bytes,
+        _native.stream_of(dev),
+    )  # fmt: skip
+    _native.check(status, what)
+    return out
+
+
+def reference_decode_attention(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    context_lens: torch.Tensor,
+    block_size: int,
+) -> torch.Tensor:
+    """Plain PyTorch gather-then-attention, one sequence at a time (reference :192-211):
+    the slow path the kernel is checked against. fp32 math, result cast to q.dtype."""
+    outs = []
+    groups = q.shape[1] // k_cache.shape[1]
+    scale = q.shape[-1] ** -0.5
+    for i in range(q.shape[0]):
+        n = int(context_lens[i])
+        pos = torch.arange(n, device=q.device)
+        slots = block_tables[i, pos // block_size].long() * block_size + pos % block_size
+        k = k_cache[slots].float().repeat_interleave(groups, dim=1).transpose(0, 1).contiguous()
+        v = v_cache[slots].float().repeat_interleave(groups, dim=1).transpose(0, 1).contiguous()
+        w = torch.softmax((k @ q[i].float()[:, :, None])[..., 0] * scale, dim=-1)  # [nh, n]
+        outs.append((w[:, None, :] @ v)[:, 0])  # [nh, hd]
+    return torch.stack(outs).to(q.dtype)

@@ -1,0 +1,168 @@
+"""CPU checks of the drop-in boundary: the C ABI library loads and exports every symbol
+include/paged_kv.h declares, its host-side validation rejects bad arguments before any
+launch, and the Python wrappers mirror the reference's signatures and errors. No
+compute call reaches a GPU here."""
+
+from __future__ import annotations
+
+import inspect
+import os
+import re
+
+import pytest
+import torch
+
+from engine import workloads
+from engine.kernels import _native
+from engine.kernels import paged_attention as pa
+from engine.runtime import paged_cache
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "paged_kv.h")
+
+
+def _declared() -> list[str]:
+    text = open(HEADER).read()
+    return re.findall(r"^\s*(?:const\s+)?[\w\s\*]+?\b(pkv_\w+)\s*\(", text, re.M)
+
+
+def test_header_symbols_are_exported_and_bound():
+    names = _declared()
+    assert len(names) >= 7
+    lib = _native.lib()
+    for name in names:
+        assert hasattr(lib, name), name
+        assert name in _native.SIGNATURES, f"{name} has no ctypes signature"
+    assert set(_native.SIGNATURES) == set(names)
+    assert lib.pkv_abi_version() == _native.ABI_VERSION
+
+
+def test_status_strings():
+    lib = _native.lib()
+    assert lib.pkv_status_string(0) == b"ok"
+    for code in (-1, -2, -3, -4, -5):
+        assert lib.pkv_status_string(code) != b"unknown error"
+
+
+def test_split_and_workspace_arithmetic():
+    lib = _native.lib()
+    assert lib.pkv_decode_num_splits(256, 32) == 8
+    assert lib.pkv_decode_num_splits(257, 32) == 9
+    assert lib.pkv_decode_num_splits(0, 32) == 1
+    assert lib.pkv_decode_workspace_bytes(64, 24, 128, 1) == 0
+    rows = 64 * 8 * 24
+    assert lib.pkv_decode_workspace_bytes(64, 24, 128, 8) >= rows * (128 + 2) * 4
+
+
+def _decode_args(**over):
+    a = dict(out=1 << 12, out_dtype=2, osb=24 * 128, osh=128, q=1 << 12, qsb=24 * 128,
+             qsh=128, k=1 << 12, v=1 << 12, kv_dtype=2, kss=1024, ksh=128, num_slots=64,
+             tables=1 << 12, tsb=4, w=4, ctx=1 << 12, batch=2, nh=24, nkv=8, hd=128, bs=16,
+             scale=0.088, split=4, ws=None, ws_bytes=0, stream=None)  # fmt: skip
+    a.update(over)
+    return list(a.values())
+
+
+@pytest.mark.parametrize(
+    ("over", "code"),
+    [({"kv_dtype": 7}, -1), ({"out_dtype": 1}, -1), ({"hd": 96}, -2), ({"nh": 20}, -2),
+     ({"split": 0}, -2), ({"split": 65}, -2), ({"bs": 0}, -2), ({"q": (1 << 12) + 2}, -3),
+     ({"kss": 1020}, -3), ({"q": None}, -5),
+     ({"w": 8, "split": 4}, -4)],
+)  # fmt: skip
+def test_decode_rejects_before_launch(over, code):
+    """Every rejection happens on the host: these calls never reach the GPU."""
+    assert _native.lib().pkv_paged_decode(*_decode_args(**over)) == code
+
+
+def test_append_and_copy_reject_before_launch():
+    lib = _native.lib()
+    # bad dtype code
+    assert lib.pkv_kv_append(1 << 12, 1 << 12, 5, 1024, 128, 64, 1 << 12, 1024, 128, 1 << 12,
+                             1024, 128, 2, 1 << 12, 4, 8, 128, None) == -1  # fmt: skip
+    # zero tokens: a no-op success
+    assert lib.pkv_kv_append(None, None, 2, 1024, 128, 64, None, 1024, 128, None, 1024, 128,
+                             2, None, 0, 8, 128, None) == 0  # fmt: skip
+    assert lib.pkv_copy_blocks(None, None, 0, 1, 4096, 8, None, 0, None) == 0
+    assert lib.pkv_copy_blocks(None, None, 0, 1, 4096, 8, None, 3, None) == -5
+    assert lib.pkv_copy_blocks(1 << 12, 1 << 12, 0, 1, 0, 8, 1 << 12, 3, None) == -2
+
+
+def test_python_signatures_mirror_reference():
+    sig = inspect.signature(pa.paged_decode_attention)
+    assert list(sig.parameters)[:7] == ["q", "k_cache", "v_cache", "block_tables",
+                                        "context_lens", "block_size", "block_n"]  # fmt: skip
+    assert sig.parameters["block_n"].default == 64
+    ref = inspect.signature(pa.reference_decode_attention)
+    assert list(ref.parameters) == ["q", "k_cache", "v_cache", "block_tables", "context_lens",
+                                    "block_size"]  # fmt: skip
+    w = inspect.signature(paged_cache.PagedKVCache.write)
+    assert list(w.parameters) == ["self", "layer", "k", "v", "slots"]
+    assert pa.HAS_TRITON is False
+    assert pa.use_gqa_kernel(torch.bfloat16, 4, 64)
+    assert not pa.use_gqa_kernel(torch.float32, 4, 64)
+    assert not pa.use_gqa_kernel(torch.bfloat16, 4, 48)
+
+
+def test_cpu_tensors_fail_loudly():
+    """No CPU fallback: the product path refuses CPU tensors instead of computing."""
+    step = workloads.custom([5, 9], 4, 2, 16, 4, torch.bfloat16)
+    assert not pa.available(torch.device("cpu"))
+    with pytest.raises(ValueError, match="GPU"):
+        pa.paged_decode_attention(step.q, step.k_cache, step.v_cache, step.block_tables,
+                                  step.context_lens, step.block_size)  # fmt: skip
+    with pytest.raises(ValueError, match="GPU"):
+        paged_cache.kv_append(step.k_cache, step.v_cache, step.new_k, step.new_v,
+                              step.slot_mapping)  # fmt: skip
+    cfg = paged_cache.KVShape(2, 2, 16)
+    cache = paged_cache.PagedKVCache(cfg, 4, 4, device="cpu")
+    with pytest.raises(ValueError, match="GPU"):
+        cache.copy_blocks(torch.tensor([[0, 1]]))
+    assert paged_cache.PagedKVCache.bytes_per_block(cfg, 4, torch.bfloat16) == 2 * 2 * 2 * 16 * 4 * 2
+
+
+def test_missing_library_raises(monkeypatch, tmp_path):
+    monkeypatch.setattr(_native, "_lib", None)
+    monkeypatch.setattr(_native, "LIB_PATH", str(tmp_path / "absent.so"))
+    with pytest.raises(RuntimeError, match="not built"):
+        _native.lib()
+
+
+def test_split_policy_is_static_and_bounded():
+    # C2: 64 seqs x 8 KV heads, W=256 blocks of 16: 512-token splits already give 4096 waves.
+    assert pa.decode_split_blocks(64, 8, 3, 256, 16) == 32
+    # C1: few sequences, short table: splits shrink to 64 tokens for parallelism.
+    assert pa.decode_split_blocks(8, 8, 4, 32, 16) == 4
+    for b, nkv, g, w, bs in [(1, 1, 1, 1, 1), (5, 2, 2, 84, 4), (32, 8, 4, 2048, 16),
+                             (3, 8, 16, 10, 1), (256, 8, 3, 193, 16)]:  # fmt: skip
+        sb = pa.decode_split_blocks(b, nkv, g, w, bs)
+        assert 1 <= sb <= 64
+
+
+def test_workload_generators_follow_engine_layout():
+    for make in (workloads.config1, workloads.config2, workloads.config4):
+        step = make("cpu", seed=1)
+        bs = step.block_size
+        tabs = step.block_tables.tolist()
+        ctx = step.context_lens.tolist()
+        used = []
+        for row, n in zip(tabs, ctx, strict=True):
+            nb = -(-n // bs)
+            assert nb <= len(row)
+            used += row[:nb]
+        assert len(used) == len(set(used)), "physical blocks must not be shared"
+        assert max(used) * bs < step.k_cache.shape[0]
+        # slot of the appended token: table[(n-1)//bs]*bs + (n-1)%bs (reference :140-143)
+        want = [row[(n - 1) // bs] * bs + (n - 1) % bs for row, n in zip(tabs, ctx, strict=True)]
+        assert step.slot_mapping.tolist() == want
+    c2 = workloads.config2("cpu", seed=0)
+    assert tuple(c2.q.shape) == (64, 24, 128) and c2.k_cache.dtype == torch.bfloat16
+    assert all(1024 <= n <= 4096 for n in c2.context_lens.tolist())
+    c3 = workloads.config3("cpu", seed=0, batch=16, cow=4)
+    shared = c3.info["shared_blocks"]
+    rows = c3.block_tables.tolist()
+    assert all(r[: shared - 1] == rows[0][: shared - 1] for r in rows)
+    src, dst = zip(*c3.cow_mapping.tolist(), strict=True)
+    assert len(set(src)) == 1 and len(set(dst)) == 4
+    assert [r[shared - 1] for r in rows[:4]] == list(dst)
+    assert c3.unique_kv_bytes() < c3.kv_bytes()

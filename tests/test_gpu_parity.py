@@ -1,0 +1,354 @@
+"""Parity of the HIP path (through the C ABI) with the CPU oracle on the same seeded
+inputs. Append and block copy: bit-exact. Attention: the unrounded fp32 result within
+max-abs 2e-3 of the oracle, and the q.dtype result equal to that fp32 result rounded
+(so within 2e-3 plus half an output ulp of the oracle).
+
+Each test prints the case it is about to run (flushed) so a failing GPU step names it.
+"""
+
+from __future__ import annotations
+
+import os
+
+import pytest
+import torch
+
+from engine import workloads
+from engine.kernels import _native
+from engine.kernels import paged_attention as pa
+from engine.runtime.paged_cache import PagedKVCache, KVShape, copy_blocks, kv_append
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+THREADS = min(16, os.cpu_count() or 1)
+ATOL = 2e-3  # max-abs error of the fp32 attention result
+
+
+def _say(*a):
+    print("[case]", *a, flush=True)
+
+
+def _bits(t: torch.Tensor) -> torch.Tensor:
+    return t.view(torch.uint8)
+
+
+def _check_attention(step, split_blocks=None, ctx_for_oracle=None, what=""):
+    """Run the kernel with fp32 and native-dtype outputs, compare with the oracle."""
+    args = (step.q, step.k_cache, step.v_cache, step.block_tables, step.context_lens,
+            step.block_size)  # fmt: skip
+    out32 = torch.empty(step.q.shape, dtype=torch.float32, device=DEV)
+    pa.paged_decode_attention(*args, out=out32, split_blocks=split_blocks)
+    outq = pa.paged_decode_attention(*args, split_blocks=split_blocks)
+    torch.cuda.synchronize()
+    ctx = step.context_lens.cpu() if ctx_for_oracle is None else ctx_for_oracle
+    want = oracle.decode_attention(step.q.cpu(), step.k_cache.cpu(), step.v_cache.cpu(),
+                                   step.block_tables.cpu(), ctx, step.block_size,
+                                   threads=THREADS)  # fmt: skip
+    err = (out32.cpu() - want).abs().max().item()
+    assert err <= ATOL, f"{what}: fp32 max|err| {err}"
+    # The q.dtype output is exactly the fp32 result rounded by torch's own conversion.
+    assert torch.equal(_bits(outq), _bits(out32.to(step.q.dtype))), f"{what}: rounding"
+    return out32, err
+
+
+# ---- KV append ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize(
+    ("pool_dt", "new_dt"),
+    [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16),
+     (torch.float32, torch.float32), (torch.bfloat16, torch.float32),
+     (torch.float16, torch.float32), (torch.float32, torch.bfloat16),
+     (torch.bfloat16, torch.float16)],
+)  # fmt: skip
+@pytest.mark.parametrize("hd", [16, 64, 128, 12])
+def test_append_bit_exact(pool_dt, new_dt, hd):
+    _say("append", pool_dt, new_dt, hd)
+    g = torch.Generator(device=DEV).manual_seed(1)
+    nslots, nkv, n = 4096, 8, 300
+    k_pool = torch.randn(nslots, nkv, hd, device=DEV, generator=g).to(pool_dt)
+    v_pool = torch.randn(nslots, nkv, hd, device=DEV, generator=g).to(pool_dt)
+    # call-site layout: transposes of [nkv, N, hd] projections
+    k = torch.randn(nkv, n, hd, device=DEV, generator=g).to(new_dt).transpose(0, 1)
+    v = torch.randn(nkv, n, hd, device=DEV, generator=g).to(new_dt).transpose(0, 1)
+    slots = torch.randperm(nslots, device=DEV, generator=g)[:n]
+    kc, vc = k_pool.cpu(), v_pool.cpu()
+    oracle.kv_append(kc, vc, k.cpu(), v.cpu(), slots.cpu())
+    want_k, want_v = k_pool.clone(), v_pool.clone()
+    want_k.index_copy_(0, slots, k.to(pool_dt))
+    want_v.index_copy_(0, slots, v.to(pool_dt))
+    kv_append(k_pool, v_pool, k, v, slots)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(k_pool.cpu()), _bits(kc)) and torch.equal(_bits(v_pool.cpu()), _bits(vc))
+    assert torch.equal(_bits(k_pool), _bits(want_k)) and torch.equal(_bits(v_pool), _bits(want_v))
+
+
+def test_append_special_values_match_device_conversion():
+    """NaN, inf, rounding ties and subnormals convert exactly as torch does on the GPU."""
+    _say("append special values")
+    vals = [float("nan"), float("inf"), float("-inf"), 0.0, -0.0, 65520.0, 1e-45, 3e38,
+            1.0 + 2.0**-9, 1.0 + 3 * 2.0**-9, 1.0 + 2.0**-11, 1.0 + 3 * 2.0**-11, 2.0**-25]  # fmt: skip
+    x = torch.tensor(vals * 2, dtype=torch.float32)  # 26 values
+    k = torch.zeros(1, 2, 16)
+    k.view(-1)[:26] = x
+    k = k.to(DEV)
+    slots = torch.tensor([3], device=DEV)
+    for pool_dt in (torch.bfloat16, torch.float16):
+        kp = torch.zeros(8, 2, 16, dtype=pool_dt, device=DEV)
+        vp = torch.zeros_like(kp)
+        kv_append(kp, vp, k, -k, slots)
+        want = torch.zeros_like(kp)
+        want.index_copy_(0, slots, k.to(pool_dt))
+        torch.cuda.synchronize()
+        assert torch.equal(_bits(kp), _bits(want)), pool_dt
+
+
+def test_append_edge_cases():
+    _say("append edge cases")
+    kp = torch.zeros(32, 2, 16, dtype=torch.bfloat16, device=DEV)
+    vp = torch.zeros_like(kp)
+    k = torch.randn(4, 2, 16, device=DEV).to(torch.bfloat16)
+    v = torch.randn(4, 2, 16, device=DEV).to(torch.bfloat16)
+    kv_append(kp, vp, k[:0], v[:0], torch.zeros(0, dtype=torch.int64, device=DEV))  # N = 0
+    assert not kp.any()
+    # Out-of-range slots are skipped, the rest land.
+    kv_append(kp, vp, k, v, torch.tensor([5, -1, 32, 31], device=DEV))
+    torch.cuda.synchronize()
+    assert torch.equal(kp[5], k[0]) and torch.equal(kp[31], k[3]) and torch.equal(vp[31], v[3])
+    assert int((kp != 0).any(-1).any(-1).sum()) == 2
+    with pytest.raises(RuntimeError, match="long"):
+        kv_append(kp, vp, k, v, torch.tensor([1, 2, 3, 4], dtype=torch.int32, device=DEV))
+    with pytest.raises(IndexError):
+        kv_append(kp, vp, k, v, torch.tensor([1, 2, 3], device=DEV))
+
+
+def test_paged_cache_write_all_layers():
+    _say("PagedKVCache.write")
+    cfg = KVShape(num_hidden_layers=3, num_key_value_heads=8, head_dim=128)
+    cache = PagedKVCache(cfg, num_blocks=64, block_size=16, device=DEV, dtype=torch.bfloat16)
+    ref = PagedKVCache(cfg, num_blocks=64, block_size=16, device=DEV, dtype=torch.bfloat16)
+    for layer in range(3):
+        k = torch.randn(64, 8, 128, device=DEV)
+        v = torch.randn(64, 8, 128, device=DEV)
+        slots = torch.randperm(1024, device=DEV)[:64]
+        cache.write(layer, k, v, slots)
+        ref.k[layer].index_copy_(0, slots, k.to(torch.bfloat16))
+        ref.v[layer].index_copy_(0, slots, v.to(torch.bfloat16))
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(cache.k), _bits(ref.k)) and torch.equal(_bits(cache.v), _bits(ref.v))
+
+
+# ---- block copy --------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize(("bs", "nkv", "hd", "dtype"),
+                         [(16, 8, 128, torch.bfloat16), (4, 2, 16, torch.float32),
+                          (1, 1, 2, torch.float16)])  # fmt: skip
+def test_copy_blocks_bit_exact(bs, nkv, hd, dtype):
+    _say("copy_blocks", bs, nkv, hd, dtype)
+    layers, nblk = 4, 200
+    cfg = KVShape(layers, nkv, hd)
+    cache = PagedKVCache(cfg, nblk, bs, device=DEV, dtype=dtype)
+    cache.k.normal_()
+    cache.v.normal_()
+    pairs = torch.tensor([[7, 100], [7, 101], [50, 3], [199, 150], [0, 250]], device=DEV)
+    kc, vc = cache.k.cpu(), cache.v.cpu()
+    oracle.copy_blocks(kc, vc, pairs.cpu(), bs)
+    cache.copy_blocks(pairs)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(cache.k.cpu()), _bits(kc)) and torch.equal(_bits(cache.v.cpu()), _bits(vc))
+
+
+def test_copy_blocks_config3_cow():
+    """Config 3's copy-on-write: 64 copies of the last shared block, then decode parity."""
+    _say("config3 CoW + decode")
+    step = workloads.config3(DEV, seed=0)
+    before = step.k_cache.clone()
+    copy_blocks(step.k_cache, step.v_cache, step.cow_mapping, step.block_size)
+    torch.cuda.synchronize()
+    bs = step.block_size
+    for s, d in step.cow_mapping.tolist():
+        assert torch.equal(_bits(step.k_cache[d * bs : (d + 1) * bs]), _bits(before[s * bs : (s + 1) * bs]))
+    kv_append(step.k_cache, step.v_cache, step.new_k, step.new_v, step.slot_mapping)
+    # oracle on a subset of sequences (8 of 256, with and without CoW)
+    idx = torch.tensor([0, 1, 63, 64, 100, 200, 254, 255])
+    sub = workloads.DecodeStep(step.name, step.q[idx], step.k_cache, step.v_cache,
+                               step.block_tables[idx], step.context_lens[idx], bs,
+                               step.new_k, step.new_v, step.slot_mapping)  # fmt: skip
+    _check_attention(sub, what="c3 subset")
+
+
+# ---- decode attention --------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize(("nh", "nkv", "hd"), [(32, 8, 64), (24, 8, 128), (4, 2, 16)])
+@pytest.mark.parametrize("block_size", [4, 16])
+def test_decode_reference_matrix(dtype, nh, nkv, hd, block_size):
+    """The reference's kernel test cases (reference tests/test_kernels.py:17-37)."""
+    _say("decode matrix", dtype, nh, nkv, hd, block_size)
+    step = workloads.custom([1, 17, 200, 64, 333], nh, nkv, hd, block_size, dtype, DEV, seed=0)
+    _check_attention(step, what="matrix")
+    # the reference's own PyTorch oracle, run on the GPU, agrees to its bf16 tolerance
+    got = pa.paged_decode_attention(step.q, step.k_cache, step.v_cache, step.block_tables,
+                                    step.context_lens, step.block_size)  # fmt: skip
+    ref = pa.reference_decode_attention(step.q, step.k_cache, step.v_cache, step.block_tables,
+                                        step.context_lens, step.block_size)  # fmt: skip
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    torch.testing.assert_close(got, ref, atol=tol, rtol=tol)
+
+
+@pytest.mark.parametrize("hd", [16, 32, 64, 128, 256])
+@pytest.mark.parametrize("groups", [1, 2, 3, 4, 5, 6, 8, 16])
+def test_decode_head_dims_and_groups(hd, groups):
+    _say("decode hd/groups", hd, groups)
+    nkv = 2
+    step = workloads.custom([3, 40, 129, 700], nkv * groups, nkv, hd, 16, torch.bfloat16, DEV,
+                            seed=hd + groups)  # fmt: skip
+    _check_attention(step, what=f"hd{hd} g{groups}")
+
+
+@pytest.mark.parametrize("block_size", [1, 2, 3, 8, 32])
+def test_decode_block_sizes(block_size):
+    _say("decode block size", block_size)
+    step = workloads.custom([1, 5, 31, 97, 260], 8, 2, 64, block_size, torch.bfloat16, DEV, seed=2)
+    _check_attention(step, what=f"bs{block_size}")
+
+
+@pytest.mark.parametrize("split_blocks", [1, 2, 3, 7, 16, 64])
+def test_decode_split_invariance(split_blocks):
+    """combine(splits) == single pass: every split size gives the oracle's answer."""
+    _say("decode split", split_blocks)
+    step = workloads.custom([1, 16, 17, 250, 1000, 2049], 24, 8, 128, 16, torch.bfloat16, DEV,
+                            seed=3)  # fmt: skip
+    _check_attention(step, split_blocks=split_blocks, what=f"split{split_blocks}")
+
+
+def test_decode_edge_cases():
+    _say("decode edge cases")
+    step = workloads.custom([0, 1, 40, 64], 8, 2, 64, 16, torch.bfloat16, DEV, seed=4, width=6)
+    out32, _ = _check_attention(step, what="ctx0")
+    assert not out32[0].any()  # empty context -> 0
+    # Context longer than the table covers: clamped to W * block_size.
+    over = step.context_lens.clone()
+    over[3] = 10_000
+    step.context_lens = over
+    _check_attention(step, ctx_for_oracle=torch.tensor([0, 1, 40, 96], dtype=torch.int32),
+                     what="ctx clamp")  # fmt: skip
+    # A block id outside the pool masks its tokens instead of faulting.
+    step.context_lens = torch.tensor([0, 1, 40, 64], dtype=torch.int32, device=DEV)
+    bad = step.block_tables.clone()
+    bad[2, 2] = 1 << 20  # third block of a 40-token sequence: positions 32..39 masked
+    step.block_tables = bad
+    _check_attention(step, ctx_for_oracle=torch.tensor([0, 1, 32, 64], dtype=torch.int32),
+                     what="oob block")  # fmt: skip
+
+
+def test_decode_table_row_stride_and_graph_padding_rows():
+    """Graph-buffer contract (reference cuda_graphs.py:39-43, :99-106): tables are a
+    view of a wider static buffer; padding rows have ctx = 1 and read a scratch block."""
+    _say("decode table stride + padding rows")
+    real = workloads.custom([50, 300, 7], 24, 8, 128, 16, torch.bfloat16, DEV, seed=5)
+    scratch = real.k_cache.shape[0] // 16 - 1
+    wide = torch.full((8, 40), scratch, dtype=torch.int32, device=DEV)
+    wide[:3, : real.block_tables.shape[1]] = real.block_tables
+    ctx = torch.ones(8, dtype=torch.int32, device=DEV)
+    ctx[:3] = real.context_lens
+    q = torch.randn(8, 24, 128, device=DEV).to(torch.bfloat16)
+    q[:3] = real.q
+    step = workloads.DecodeStep("padded", q, real.k_cache, real.v_cache, wide[:, :20], ctx, 16,
+                                real.new_k, real.new_v, real.slot_mapping)  # fmt: skip
+    assert step.block_tables.stride(0) == 40
+    _check_attention(step, what="padded")
+
+
+@pytest.mark.parametrize("name", ["c1", "c2"])
+def test_decode_configs_full(name):
+    """Configs 1 and 2 at full size: append, then decode attention, vs the oracle."""
+    _say("config", name)
+    step = workloads.CONFIGS[name](DEV, seed=0)
+    kc, vc = step.k_cache.cpu(), step.v_cache.cpu()
+    oracle.kv_append(kc, vc, step.new_k.cpu(), step.new_v.cpu(), step.slot_mapping.cpu())
+    kv_append(step.k_cache, step.v_cache, step.new_k, step.new_v, step.slot_mapping)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(step.k_cache.cpu()), _bits(kc))
+    assert torch.equal(_bits(step.v_cache.cpu()), _bits(vc))
+    _check_attention(step, what=name)
+
+
+def test_decode_config4_long_context():
+    """Config 4 (log-uniform up to 32k tokens): full-size split invariance, and the
+    oracle on the longest and shortest sequences."""
+    _say("config4")
+    step = workloads.config4(DEV, seed=0)
+    args = (step.q, step.k_cache, step.v_cache, step.block_tables, step.context_lens, 16)
+    outs = []
+    for sb in (4, 32, 64):
+        o = torch.empty(step.q.shape, dtype=torch.float32, device=DEV)
+        pa.paged_decode_attention(*args, out=o, split_blocks=sb)
+        outs.append(o)
+    torch.cuda.synchronize()
+    for o in outs[1:]:
+        assert (o - outs[0]).abs().max().item() < 1e-5
+    order = step.context_lens.argsort().cpu()
+    idx = torch.cat([order[:2], order[-2:]])
+    sub = workloads.DecodeStep(step.name, step.q[idx], step.k_cache, step.v_cache,
+                               step.block_tables[idx], step.context_lens[idx], 16,
+                               step.new_k, step.new_v, step.slot_mapping)  # fmt: skip
+    _check_attention(sub, what="c4 subset")
+
+
+def test_graph_capture_replay():
+    """Append + decode captured once in a hipGraph, replayed with new lengths and tables
+    (the DecodeGraphs pattern, reference engine/runtime/cuda_graphs.py:64-108)."""
+    _say("graph capture")
+    b, nh, nkv, hd, bs, width, nblk = 16, 24, 8, 128, 16, 64, 1200
+    k_pool = torch.randn(nblk * bs, nkv, hd, device=DEV).to(torch.bfloat16)
+    v_pool = torch.randn_like(k_pool)
+    q_s = torch.zeros(b, nh, hd, device=DEV, dtype=torch.bfloat16)
+    tables_s = torch.zeros(b, width, dtype=torch.int32, device=DEV)
+    ctx_s = torch.ones(b, dtype=torch.int32, device=DEV)
+    slots_s = torch.zeros(b, dtype=torch.int64, device=DEV)
+    nk_s = torch.zeros(b, nkv, hd, device=DEV, dtype=torch.bfloat16)
+    nv_s = torch.zeros_like(nk_s)
+    out_s = torch.empty(b, nh, hd, device=DEV, dtype=torch.bfloat16)
+
+    def body():
+        kv_append(k_pool, v_pool, nk_s, nv_s, slots_s)
+        pa.paged_decode_attention(q_s, k_pool, v_pool, tables_s, ctx_s, bs, out=out_s)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        body()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        body()
+
+    for rep in range(3):
+        g = torch.Generator().manual_seed(100 + rep)
+        ctx = torch.randint(1, width * bs + 1, (b,), generator=g, dtype=torch.int32)
+        perm = torch.randperm(nblk, generator=g)[: b * width].view(b, width).int()
+        slots = perm[torch.arange(b), (ctx - 1) // bs].long() * bs + (ctx - 1) % bs
+        q_s.copy_(torch.randn(b, nh, hd, generator=g).to(torch.bfloat16))
+        tables_s.copy_(perm)
+        ctx_s.copy_(ctx)
+        slots_s.copy_(slots)
+        nk_s.copy_(torch.randn(b, nkv, hd, generator=g).to(torch.bfloat16))
+        nv_s.copy_(torch.randn(b, nkv, hd, generator=g).to(torch.bfloat16))
+        graph.replay()
+        torch.cuda.synchronize()
+        got = out_s.clone()
+        # eager on the same (already appended) pool
+        want = pa.paged_decode_attention(q_s, k_pool, v_pool, tables_s, ctx_s, bs)
+        torch.cuda.synchronize()
+        assert torch.equal(_bits(got), _bits(want)), f"replay {rep}"
+        assert torch.equal(_bits(k_pool[slots_s]), _bits(nk_s))
+
+
+def test_native_library_is_loaded_from_tree():
+    lib = _native.lib()
+    assert os.path.samefile(lib._name, _native.LIB_PATH)
+    assert pa.available(DEV)
