@@ -2,7 +2,7 @@
 
     python bench.py [--steps K] [--warmup W] [--config c2] [--layers L]
 
-A step is one layer-step of paged decode attention (split-K pass + combine) over the
+A step is one layer-step of paged decode attention (stream-K pass + combine) over the
 config's batch, on cuda:0. L independent layer pools (default 4, ~1 GB each at config 2)
 are used in rotation, so every step reads K/V that the previous step did not touch,
 as consecutive layers of a model do; the 256 MB last-level cache cannot serve them.
@@ -38,7 +38,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4"])
     ap.add_argument("--layers", type=int, default=4)
-    ap.add_argument("--split-blocks", type=int, default=None)
+    ap.add_argument("--workgroups", type=int, default=None)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -97,13 +97,13 @@ def main() -> int:
     b, nh, hd = step.q.shape
     nkv = step.k_cache.shape[1]
     w = step.block_tables.shape[1]
-    split = args.split_blocks or pa.decode_split_blocks(b, nkv, nh // nkv, w, step.block_size)
+    wgs = args.workgroups or pa.decode_workgroups(dev, step.q.dtype, hd, nh, nkv)
     out = torch.empty_like(step.q)
 
     def attn(i: int) -> None:
         k, v = pools[i % len(pools)]
         pa.paged_decode_attention(step.q, k, v, step.block_tables, step.context_lens,
-                                  step.block_size, out=out, split_blocks=split)  # fmt: skip
+                                  step.block_size, out=out, num_workgroups=wgs)  # fmt: skip
 
     for i in range(args.warmup):
         attn(i)
@@ -158,7 +158,7 @@ def main() -> int:
             "block_size": step.block_size,
             "table_width": w,
             "sum_ctx": int(step.context_lens.sum()),
-            "split_blocks": split,
+            "workgroups": wgs,
             "layer_pools": len(pools),
         },
         "roofline": {

@@ -32,6 +32,7 @@ extern "C" {
 #define PKV_E_ALIGN (-3)     /* pointer or stride not aligned for 16-byte vector access */
 #define PKV_E_WORKSPACE (-4) /* split-K workspace missing or too small */
 #define PKV_E_NULL (-5)      /* required pointer is NULL */
+#define PKV_E_HIP (-6)       /* a HIP device query failed (no usable GPU) */
 
 /* ABI version, bumped on any signature change. */
 int pkv_abi_version(void);
@@ -70,29 +71,34 @@ int pkv_copy_blocks(void* k_pool, void* v_pool, int64_t layer_stride_bytes,
                     const int64_t* block_mapping, int64_t n_pairs, void* stream);
 
 /*
- * Number of context splits the decode kernel uses for a block table of max_blocks
- * columns when each split covers split_blocks blocks (1 <= split_blocks <= 64).
+ * Workgroups the decode kernel should use on the current device for this shape: as
+ * many as the GPU holds resident at once (CUs x workgroups per CU). Depends only on the
+ * device and static shapes, so a graph captured with it stays valid. Returns >= 1, or a
+ * negative PKV_E_* code.
  */
-int32_t pkv_decode_num_splits(int32_t max_blocks, int32_t split_blocks);
+int32_t pkv_decode_workgroups(int kv_dtype, int32_t head_dim, int32_t num_heads,
+                              int32_t num_kv_heads);
 
-/* Workspace bytes pkv_paged_decode needs (0 when num_splits == 1). */
-int64_t pkv_decode_workspace_bytes(int32_t batch, int32_t num_heads, int32_t head_dim,
-                                   int32_t num_splits);
+/* Workspace bytes pkv_paged_decode needs for num_workgroups (0 when it is 1). */
+int64_t pkv_decode_workspace_bytes(int32_t num_workgroups, int32_t num_heads,
+                                   int32_t head_dim);
 
 /*
- * Paged decode attention (GQA, split-K flash decoding + combine). Replaces
- * paged_decode_attention and its Triton kernels (reference
- * engine/kernels/paged_attention.py:44-179). For sequence b and query head h:
+ * Paged decode attention (GQA). Replaces paged_decode_attention and its Triton kernels
+ * (reference engine/kernels/paged_attention.py:44-179). For sequence b and query head h:
  *   n    = clamp(context_lens[b], 0, max_blocks * block_size)
  *   slot = block_tables[b, p / block_size] * block_size + p % block_size, p < n
  *   out[b, h] = softmax_p(scale * q[b,h] . k[slot_p, h / G]) @ v[slot_p, h / G]
- * with G = num_heads / num_kv_heads, fp32 softmax and accumulation. n == 0 gives 0.
+ * with G = num_heads / num_kv_heads, fp32 softmax and accumulation; n == 0 gives 0.
+ * Tokens whose slot falls outside [0, num_slots) are left out of the softmax.
  * q: [batch, num_heads, head_dim] in kv_dtype; out: same shape, kv_dtype or PKV_F32.
  * k_cache / v_cache share strides (stride_slot, stride_head, 1).
  * block_tables: int32 [batch, >= max_blocks] with row stride table_stride.
- * head_dim in {16, 32, 64, 128, 256}; split_blocks in [1, 64]. When
- * pkv_decode_num_splits(max_blocks, split_blocks) > 1 the caller passes a workspace of
- * at least pkv_decode_workspace_bytes(...) bytes (any contents).
+ * head_dim in {16, 32, 64, 128, 256}.
+ * Work split: the contexts of all sequences, laid end to end, are divided evenly among
+ * num_workgroups workgroups (pkv_decode_workgroups gives the default); sequences cut
+ * by a boundary are merged by a second kernel. num_workgroups > 1 needs a workspace of
+ * pkv_decode_workspace_bytes(...) bytes (any contents, 16-byte aligned).
  */
 int pkv_paged_decode(void* out, int out_dtype, int64_t out_stride_b, int64_t out_stride_h,
                      const void* q, int64_t q_stride_b, int64_t q_stride_h,
@@ -101,7 +107,7 @@ int pkv_paged_decode(void* out, int out_dtype, int64_t out_stride_b, int64_t out
                      const int32_t* block_tables, int64_t table_stride, int32_t max_blocks,
                      const int32_t* context_lens, int32_t batch, int32_t num_heads,
                      int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
-                     float scale, int32_t split_blocks, void* workspace,
+                     float scale, int32_t num_workgroups, void* workspace,
                      int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus

@@ -34,8 +34,8 @@ SIGNATURES: dict[str, tuple] = {
          ctypes.c_int, _p, _i64, _i32, _i32, _p],
     ),  # fmt: skip
     "pkv_copy_blocks": (ctypes.c_int, [_p, _p, _i64, _i32, _i64, _i64, _p, _i64, _p]),
-    "pkv_decode_num_splits": (_i32, [_i32, _i32]),
-    "pkv_decode_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32]),
+    "pkv_decode_workgroups": (_i32, [ctypes.c_int, _i32, _i32, _i32]),
+    "pkv_decode_workspace_bytes": (_i64, [_i32, _i32, _i32]),
     "pkv_paged_decode": (
         ctypes.c_int,
         [_p, ctypes.c_int, _i64, _i64,            # out
@@ -43,7 +43,7 @@ SIGNATURES: dict[str, tuple] = {
          _p, _p, ctypes.c_int, _i64, _i64, _i64,  # k, v caches
          _p, _i64, _i32,                          # block tables
          _p, _i32, _i32, _i32, _i32, _i32,        # ctx, batch, nh, nkv, hd, bs
-         _f32, _i32, _p, _i64, _p],               # scale, split, workspace, stream
+         _f32, _i32, _p, _i64, _p],               # scale, wgs, workspace, stream
     ),  # fmt: skip
 }
 

@@ -4,17 +4,19 @@
 ``paged_decode_attention`` runs two hand-written HIP kernels through the C ABI of
 lib/libpaged_kv.so:
 
-1. a split-K pass: one wave per (sequence, KV head, context split) streams the split's
-   K/V rows straight from the paged pool through the block table with 16-byte loads,
-   computes the scores of every query head sharing that KV head (GQA: each K/V row is
-   read once for the whole group), and keeps an fp32 online softmax. A sequence whose
-   context fits one split writes its output directly.
-2. a combine pass that merges the splits of longer contexts with log-sum-exp weights.
+1. a stream-K pass: the contexts of all sequences, laid end to end, are split evenly
+   over as many workgroups as the GPU holds at once. One wave per KV head streams its
+   share of K/V rows straight from the paged pool through the block table with
+   16-byte non-temporal loads, computes the scores of every query head sharing that KV
+   head (GQA: each K/V row is read once for the whole group), and keeps an fp32 online
+   softmax. Sequences that lie inside one workgroup's share are written directly.
+2. a combine pass that merges, with log-sum-exp weights, the pieces of the sequences
+   cut by a share boundary.
 
-The number of splits depends only on the block-table width (a static shape), never on
-the context lengths (device data), so one hipGraph capture serves every length, as the
-reference's CUDA-graph decode requires (reference engine/runtime/cuda_graphs.py:10-11).
-Nothing here allocates outside torch's caching allocator or synchronises.
+The grid depends only on the device and static shapes, never on the context lengths
+(device data), so one hipGraph capture serves every length, as the reference's
+CUDA-graph decode requires (reference engine/runtime/cuda_graphs.py:10-11). Nothing here
+allocates outside torch's caching allocator or synchronises.
 """
 
 from __future__ import annotations
@@ -28,9 +30,7 @@ from engine.kernels import _native
 HAS_TRITON = False
 
 SUPPORTED_HEAD_DIMS = (16, 32, 64, 128, 256)
-_WAVES_TARGET = 2048  # ~8 waves per CU on 256 CUs
-_SPLIT_TOKENS_MAX = 512
-_SPLIT_TOKENS_MIN = 64
+_default_wgs: dict[tuple, int] = {}
 
 
 def available(device: torch.device) -> bool:
@@ -56,20 +56,21 @@ def use_gqa_kernel(dtype: torch.dtype, groups: int, head_dim: int) -> bool:
     )
 
 
-def decode_split_blocks(batch: int, num_kv_heads: int, groups: int, max_blocks: int,
-                        block_size: int) -> int:  # fmt: skip
-    """Blocks per context split. Static shapes only (graph-safe). Splits are at most
-    512 tokens; they shrink (down to 64 tokens) until the grid offers ~2048 waves."""
-    heads_per_wave = groups if groups <= 4 else next(
-        (c for c in (4, 3, 2) if groups % c == 0), 1
-    )  # fmt: skip
-    tasks = batch * num_kv_heads * (groups // heads_per_wave)
-    hi = max(1, min(64, _SPLIT_TOKENS_MAX // block_size))
-    lo = max(1, min(hi, _SPLIT_TOKENS_MIN // block_size))
-    sb = hi
-    while sb > lo and tasks * -(-max(max_blocks, 1) // sb) < _WAVES_TARGET:
-        sb //= 2
-    return max(sb, lo)
+def decode_workgroups(device: torch.device, dtype: torch.dtype, head_dim: int,
+                      num_heads: int, num_kv_heads: int) -> int:  # fmt: skip
+    """Workgroups the decode kernel uses by default: as many as ``device`` holds at once
+    for this shape (a device property, so graph captures stay valid). Cached."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    key = (idx, dtype, head_dim, num_heads, num_kv_heads)
+    wgs = _default_wgs.get(key)
+    if wgs is None:
+        with torch.cuda.device(idx):
+            wgs = _native.lib().pkv_decode_workgroups(
+                _native.dtype_code(dtype, "decode_workgroups"), head_dim, num_heads,
+                num_kv_heads)  # fmt: skip
+        _native.check(min(wgs, 0), "decode_workgroups")
+        _default_wgs[key] = wgs
+    return wgs
 
 
 def paged_decode_attention(
@@ -82,7 +83,7 @@ def paged_decode_attention(
     block_n: int = 64,
     *,
     out: torch.Tensor | None = None,
-    split_blocks: int | None = None,
+    num_workgroups: int | None = None,
 ) -> torch.Tensor:
     """q: [B, nh, hd]; k_cache, v_cache: [num_slots, nkv, hd] (one layer);
     block_tables: [B, max_blocks] int32; context_lens: [B] int32 -> [B, nh, hd].
@@ -90,7 +91,8 @@ def paged_decode_attention(
     Reference: engine/kernels/paged_attention.py:140-179. ``block_n`` (the reference's
     Triton tile) is accepted and ignored. Extensions: ``out`` receives the result in
     place ([B, nh, hd], q.dtype or float32 for the unrounded fp32 result) and
-    ``split_blocks`` overrides the context split size (1..64 blocks).
+    ``num_workgroups`` overrides how many workgroups share the contexts (default: as many
+    as the GPU holds at once).
     """
     del block_n
     what = "paged_decode_attention"
@@ -131,12 +133,10 @@ def paged_decode_attention(
         return out
 
     max_blocks = block_tables.shape[1]
-    groups = nh // nkv
-    if split_blocks is None:
-        split_blocks = decode_split_blocks(b, nkv, groups, max_blocks, block_size)
+    if num_workgroups is None:
+        num_workgroups = decode_workgroups(dev, q.dtype, hd, nh, nkv)
     lib = _native.lib()
-    splits = lib.pkv_decode_num_splits(max_blocks, split_blocks)
-    ws_bytes = lib.pkv_decode_workspace_bytes(b, nh, hd, splits)
+    ws_bytes = lib.pkv_decode_workspace_bytes(num_workgroups, nh, hd)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
     status = lib.pkv_paged_decode(
         out.data_ptr(), _native.dtype_code(out.dtype, what), out.stride(0), out.stride(1),
@@ -145,7 +145,7 @@ def paged_decode_attention(
         k_cache.stride(0), k_cache.stride(1), k_cache.shape[0],
         block_tables.data_ptr(), block_tables.stride(0), max_blocks,
         context_lens.data_ptr(), b, nh, nkv, hd, block_size,
-        hd**-0.5, split_blocks, ws.data_ptr() if ws is not None else None, ws_bytes,
+        hd**-0.5, num_workgroups, ws.data_ptr() if ws is not None else None, ws_bytes,
         _native.stream_of(dev),
     )  # fmt: skip
     _native.check(status, what)

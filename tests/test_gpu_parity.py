@@ -33,13 +33,13 @@ def _bits(t: torch.Tensor) -> torch.Tensor:
     return t.view(torch.uint8)
 
 
-def _check_attention(step, split_blocks=None, ctx_for_oracle=None, what=""):
+def _check_attention(step, wgs=None, ctx_for_oracle=None, what=""):
     """Run the kernel with fp32 and native-dtype outputs, compare with the oracle."""
     args = (step.q, step.k_cache, step.v_cache, step.block_tables, step.context_lens,
             step.block_size)  # fmt: skip
     out32 = torch.empty(step.q.shape, dtype=torch.float32, device=DEV)
-    pa.paged_decode_attention(*args, out=out32, split_blocks=split_blocks)
-    outq = pa.paged_decode_attention(*args, split_blocks=split_blocks)
+    pa.paged_decode_attention(*args, out=out32, num_workgroups=wgs)
+    outq = pa.paged_decode_attention(*args, num_workgroups=wgs)
     torch.cuda.synchronize()
     ctx = step.context_lens.cpu() if ctx_for_oracle is None else ctx_for_oracle
     want = oracle.decode_attention(step.q.cpu(), step.k_cache.cpu(), step.v_cache.cpu(),
@@ -216,13 +216,15 @@ def test_decode_block_sizes(block_size):
     _check_attention(step, what=f"bs{block_size}")
 
 
-@pytest.mark.parametrize("split_blocks", [1, 2, 3, 7, 16, 64])
-def test_decode_split_invariance(split_blocks):
-    """combine(splits) == single pass: every split size gives the oracle's answer."""
-    _say("decode split", split_blocks)
-    step = workloads.custom([1, 16, 17, 250, 1000, 2049], 24, 8, 128, 16, torch.bfloat16, DEV,
-                            seed=3)  # fmt: skip
-    _check_attention(step, split_blocks=split_blocks, what=f"split{split_blocks}")
+@pytest.mark.parametrize("wgs", [1, 2, 3, 7, 16, 64, 255, 1000, 5000])
+def test_decode_partition_invariance(wgs):
+    """combine(pieces) == single pass: every way of cutting the contexts among
+    workgroups (including more workgroups than work units) gives the oracle's answer."""
+    _say("decode workgroups", wgs)
+    step = workloads.custom([1, 16, 17, 250, 1000, 2049, 0, 5], 24, 8, 128, 16,
+                            torch.bfloat16, DEV, seed=3)  # fmt: skip
+    out32, _ = _check_attention(step, wgs=wgs, what=f"wgs{wgs}")
+    assert not out32[6].any()
 
 
 def test_decode_edge_cases():
@@ -240,9 +242,14 @@ def test_decode_edge_cases():
     step.context_lens = torch.tensor([0, 1, 40, 64], dtype=torch.int32, device=DEV)
     bad = step.block_tables.clone()
     bad[2, 2] = 1 << 20  # third block of a 40-token sequence: positions 32..39 masked
+    bad[1, 0] = -7  # the only block of the 1-token sequence: nothing left, output 0
     step.block_tables = bad
-    _check_attention(step, ctx_for_oracle=torch.tensor([0, 1, 32, 64], dtype=torch.int32),
-                     what="oob block")  # fmt: skip
+    # Every way of cutting the work, so a piece may start (or consist of) masked tiles.
+    for wgs in (None, 1, 2, 5, 9, 64):
+        out32, _ = _check_attention(
+            step, wgs=wgs, ctx_for_oracle=torch.tensor([0, 0, 32, 64], dtype=torch.int32),
+            what=f"oob block wgs={wgs}")  # fmt: skip
+        assert not out32[1].any()
 
 
 def test_decode_table_row_stride_and_graph_padding_rows():
@@ -278,15 +285,15 @@ def test_decode_configs_full(name):
 
 
 def test_decode_config4_long_context():
-    """Config 4 (log-uniform up to 32k tokens): full-size split invariance, and the
+    """Config 4 (log-uniform up to 32k tokens): full-size partition invariance, and the
     oracle on the longest and shortest sequences."""
     _say("config4")
     step = workloads.config4(DEV, seed=0)
     args = (step.q, step.k_cache, step.v_cache, step.block_tables, step.context_lens, 16)
     outs = []
-    for sb in (4, 32, 64):
+    for wgs in (None, 97, 1024):
         o = torch.empty(step.q.shape, dtype=torch.float32, device=DEV)
-        pa.paged_decode_attention(*args, out=o, split_blocks=sb)
+        pa.paged_decode_attention(*args, out=o, num_workgroups=wgs)
         outs.append(o)
     torch.cuda.synchronize()
     for o in outs[1:]:
