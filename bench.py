@@ -42,6 +42,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run 5 plain 1 GiB device-to-device copies: the known-size "
+                         "kernel that scales rocprofv3's FETCH_SIZE / WRITE_SIZE")  # fmt: skip
     return ap.parse_args()
 
 
@@ -173,6 +176,13 @@ def main() -> int:
         "median_us": round(statistics.median(per), 2),
         "append_us": round(append_us, 2),
     }
+    if args.copy_calibration:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(step, args.cpu_seconds)
     print(json.dumps(line), flush=True)
