@@ -79,8 +79,10 @@ int pkv_copy_blocks(void* k_pool, void* v_pool, int64_t layer_stride_bytes,
 int32_t pkv_decode_workgroups(int kv_dtype, int32_t head_dim, int32_t num_heads,
                               int32_t num_kv_heads);
 
-/* Workspace bytes pkv_paged_decode needs for num_workgroups (0 when it is 1). */
-int64_t pkv_decode_workspace_bytes(int32_t num_workgroups, int32_t num_heads,
+/* Bytes of scratch pkv_paged_decode needs for num_workgroups (0 when it is 1): one
+ * 16-byte merge plan per sequence, then the partial records of sequences cut by a
+ * range boundary. Any contents. */
+int64_t pkv_decode_workspace_bytes(int32_t num_workgroups, int32_t batch, int32_t num_heads,
                                    int32_t head_dim);
 
 /*
@@ -96,9 +98,9 @@ int64_t pkv_decode_workspace_bytes(int32_t num_workgroups, int32_t num_heads,
  * block_tables: int32 [batch, >= max_blocks] with row stride table_stride.
  * head_dim in {16, 32, 64, 128, 256}.
  * Work split: the contexts of all sequences, laid end to end, are divided evenly among
- * num_workgroups workgroups (pkv_decode_workgroups gives the default); sequences cut
- * by a boundary are merged by a second kernel. num_workgroups > 1 needs a workspace of
- * pkv_decode_workspace_bytes(...) bytes (any contents, 16-byte aligned).
+ * num_workgroups workgroups (pkv_decode_workgroups gives the default); a second kernel
+ * merges the pieces of sequences cut by a boundary. num_workgroups > 1 needs a 16-byte
+ * aligned scratch `workspace` of pkv_decode_workspace_bytes() bytes (any contents).
  */
 int pkv_paged_decode(void* out, int out_dtype, int64_t out_stride_b, int64_t out_stride_h,
                      const void* q, int64_t q_stride_b, int64_t q_stride_h,

@@ -8,6 +8,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "paged_kv.h"
 
 namespace {
@@ -23,6 +25,12 @@ constexpr int kWave = 64;
 #endif
 #ifndef PKV_DECODE_STREAM_LOADS
 #define PKV_DECODE_STREAM_LOADS 1
+#endif
+#ifndef PKV_DECODE_USE_MFMA
+#define PKV_DECODE_USE_MFMA 1
+#endif
+#ifndef PKV_DECODE_PREFETCH
+#define PKV_DECODE_PREFETCH 1
 #endif
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
@@ -310,6 +318,7 @@ struct DecodeArgs {
   int32_t unit_tokens;  // TILE of the instantiated kernel
   int32_t num_wg;       // workgroups along x sharing the unit stream
   float scale_log2;     // scale * log2(e)
+  int4* desc;           // [batch] per-sequence merge plan (see SeqDesc)
   float* ws_acc;        // [num_wg, 2, nh, HD] partial records
   float* ws_ml;         // [num_wg, 2, nh, 2]   their (max, sum)
   int out_f32;
@@ -362,6 +371,17 @@ __device__ __forceinline__ int64_t wg_of_unit(int64_t u, int64_t units, int64_t 
   return ((u + 1) * wgs - 1) / units;
 }
 
+// Merge plan of one sequence, written by the workgroup that holds its first unit (so
+// every sequence gets exactly one, every call): the first workgroup w0 of its pieces,
+// the number of workgroups w0..w1 it spans (1: written directly), the record slot its
+// piece has in w0, and whether every range is non-empty (units >= workgroups).
+__device__ __forceinline__ void write_desc(const DecodeArgs& a, int b, int w, int64_t ub,
+                                           int64_t ue, int64_t rs, int64_t total) {
+  if (!a.desc) return;
+  const int64_t w1 = wg_of_unit(ue - 1, total, a.num_wg);
+  a.desc[b] = make_int4(w, (int)(w1 - w + 1), rs < ub ? 1 : 0, total >= a.num_wg ? 1 : 0);
+}
+
 template <int DT, int HD, int GPW>
 __global__ void __launch_bounds__(512)
 paged_decode_stream_kernel(const DecodeArgs a) {
@@ -398,6 +418,7 @@ paged_decode_stream_kernel(const DecodeArgs a) {
     const int slot = (u == rs) ? 0 : 1;  // which record a cut piece goes to
     const int t0 = (int)(u - ub) * a.unit_tokens;
     const int t1 = min(n, (int)(seg_end - ub) * a.unit_tokens);
+    if (u == ub && task == 0 && lane == 0) write_desc(a, b, w, ub, ue, rs, total);
     u = seg_end;
     ub = ue;
 
@@ -554,113 +575,441 @@ paged_decode_stream_kernel(const DecodeArgs a) {
   }
 }
 
-// Second stage: one wave per (sequence, query head). A sequence whose units span
-// workgroups w0..w1 (w0 < w1) has one record in each non-empty range among them (in
-// w0 it is the range's last piece, slot 1, unless the range starts with it); they are
-// merged with log-sum-exp weights w_j = exp2(m_j - max m), out = sum w_j acc_j /
-// sum w_j l_j. Lane j holds record j's weight; eight records are loaded per step.
-template <int DTO>
+// ---------------------------------------------------------------------------------
+// MFMA variant of the stream pass for 16-bit K/V at head_dim 128 (the Llama-3 shapes).
+//
+// Same stream-K ranges, records and outputs as paged_decode_stream_kernel; only the
+// per-tile arithmetic differs. A tile is 16 tokens. Lane l is (col = l % 16, grp =
+// l / 16).
+//   * Scores on the matrix cores: S[16 tokens x 16 cols] = K_tile . Q^T with four
+//     v_mfma_f32_16x16x32 (32 head dims each). A operand: lane (t, g) holds K[token t]
+//     dims 32m + 8g .. +8 (one 16-byte load per MFMA); B operand: lane (j, g) holds
+//     Q[head j] at the same dims (zero for j >= GPW). Result: lane (j, g) holds the
+//     scores of tokens 4g + r (r < 4) for query head j.
+//   * Softmax in that layout: per-head max over the 16 tokens with two permlane swaps
+//     (v_permlane16/32_swap give {x[l], x[l^16]} / {x[l], x[l^32]}: no LDS trip).
+//   * PV on the VALU in fp32: lane (c, g) holds V[token 4g + r] dims 8c .. +8; each
+//     head's probabilities reach it with DPP row_newbcast (lane h of each 16-lane row
+//     to the whole row), since token 4g + r's score sits in lane (h, g) of that row.
+// When block_size is a multiple of 16 a tile lies inside one block: its block id is
+// read with v_readlane into a scalar and every lane's address is a fixed offset from it.
+// ---------------------------------------------------------------------------------
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <int DT> struct Mfma16x16x32;
+template <> struct Mfma16x16x32<PKV_BF16> {
+  typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+  __device__ static f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8, a),
+                                                   __builtin_bit_cast(v8, b), c, 0, 0, 0);
+  }
+};
+template <> struct Mfma16x16x32<PKV_F16> {
+  typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+  __device__ static f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8, a),
+                                                  __builtin_bit_cast(v8, b), c, 0, 0, 0);
+  }
+};
+
+__device__ __forceinline__ u32x4 load_kv16v(const void* p) {
+#if PKV_DECODE_STREAM_LOADS
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+#else
+  return *reinterpret_cast<const u32x4*>(p);
+#endif
+}
+
+template <int DT> __device__ __forceinline__ void unpack16v(u32x4 r, float* f) {
+  unpack16<DT>(make_uint4(r.x, r.y, r.z, r.w), f);
+}
+
+// Lane h of every 16-lane row, broadcast to its row (DPP row_newbcast).
+template <int H> __device__ __forceinline__ float row_bcast(float x) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x150 + H, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row_bcast(float x, int h) {
+  switch (h) {
+    case 0: return row_bcast<0>(x);
+    case 1: return row_bcast<1>(x);
+    case 2: return row_bcast<2>(x);
+    default: return row_bcast<3>(x);
+  }
+}
+
+// Reductions over lanes l, l^16, l^32, l^48 (the four rows of a column).
+__device__ __forceinline__ float rows_max(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float rows_sum(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+template <int DT, int GPW, bool FAST>
+__global__ void __launch_bounds__(512)
+paged_decode_mfma_kernel(const DecodeArgs a) {
+  constexpr int HD = 128, TILE = 16;
+  static_assert(GPW >= 1 && GPW <= 4, "at most 4 query heads per wave");
+  using S = typename Elt<DT>::S;
+  using MMA = Mfma16x16x32<DT>;
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int task = blockIdx.y * (blockDim.x / kWave) + (threadIdx.x / kWave);
+  const int kvh = task / a.nsub;
+  if (kvh >= a.nkv) return;
+  const int h0 = kvh * a.groups + (task - kvh * a.nsub) * GPW;
+  const int w = blockIdx.x;
+
+  int64_t total;
+  find_unit(a, -1, &total);
+  const int64_t rs = range_start(w, total, a.num_wg);
+  const int64_t re = range_start(w + 1, total, a.num_wg);
+  if (rs >= re) return;
+  int64_t ub;
+  int b = find_unit(a, rs, &ub);
+
+  const int col = lane & 15, grp = lane >> 4;
+  // FAST: block_size is a multiple of 16, so a tile never crosses a block.
+  const S* kbase = reinterpret_cast<const S*>(a.k) + (int64_t)kvh * a.kv_sh;
+  const S* vbase = reinterpret_cast<const S*>(a.v) + (int64_t)kvh * a.kv_sh;
+  // Fixed per-lane element offsets from a tile's first slot (fast path).
+  const int64_t k_off = col * a.kv_ss + 8 * grp;
+  int64_t v_off[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) v_off[r] = (4 * grp + r) * a.kv_ss + 8 * col;
+
+  for (int64_t u = rs; u < re && b < a.batch; ++b) {
+    const int n = clamped_ctx(a, b);
+    const int64_t ue = ub + units_of(a, n);
+    const int64_t seg_end = ue < re ? ue : re;
+    const bool whole = (u == ub) && (seg_end == ue);
+    const int slot = (u == rs) ? 0 : 1;
+    const int t0 = (int)(u - ub) * TILE;
+    const int t1 = min(n, (int)(seg_end - ub) * TILE);
+    if (u == ub && task == 0 && lane == 0) write_desc(a, b, w, ub, ue, rs, total);
+    u = seg_end;
+    ub = ue;
+
+    // Q^T as the B operand: column col = query head h0 + col.
+    u32x4 qb[4];
+    {
+      const S* qp = reinterpret_cast<const S*>(a.q) + b * a.q_sb + (int64_t)(h0 + col) * a.q_sh + 8 * grp;
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+        qb[m] = col < GPW ? *reinterpret_cast<const u32x4*>(qp + 32 * m) : u32x4{0, 0, 0, 0};
+    }
+
+    int cb = 0, tbl = 0;
+    auto load_table = [&](int first_block) {
+      cb = first_block;
+      const int j = cb + lane;
+      tbl = j < a.max_blocks ? a.tables[b * a.table_stride + j] : 0;
+    };
+    auto block_of = [&](int p) { return a.bs_shift >= 0 ? (p >> a.bs_shift) : p / a.bs; };
+
+    // Issue a tile's K (MFMA A layout) and V (row layout) loads; returns, per lane,
+    // bit r set when token 4*grp + r of the tile is live.
+    auto load_tile = [&](int tb, u32x4* kr, u32x4* vr) -> unsigned {
+      const u32x4 z = {0, 0, 0, 0};
+      if (tb >= t1) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kr[i] = vr[i] = z;
+        return 0;
+      }
+      if (block_of(min(tb + TILE, t1) - 1) - cb >= kWave) load_table(block_of(tb));
+      unsigned ok = 0;
+      if constexpr (FAST) {
+        const int blk = block_of(tb);
+        const int bid = __builtin_amdgcn_readlane(tbl, blk - cb);
+        const int64_t slot0 = (int64_t)bid * a.bs + (tb - blk * a.bs);
+        const int live = (bid >= 0 && slot0 + TILE <= a.num_slots) ? min(TILE, t1 - tb) : 0;
+        const S* kt = kbase + slot0 * a.kv_ss;
+        const S* vt = vbase + slot0 * a.kv_ss;
+        if (live == TILE) {  // full tile: every lane loads, no predication
+#pragma unroll
+          for (int m = 0; m < 4; ++m) kr[m] = load_kv16v(kt + k_off + 32 * m);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) vr[r] = load_kv16v(vt + v_off[r]);
+          return 0xFu;
+        }
+        if (live == 0) {  // block id outside the pool: the tile is masked
+#pragma unroll
+          for (int i = 0; i < 4; ++i) kr[i] = vr[i] = z;
+          return 0;
+        }
+        // Last, partial tile of a piece: lanes past the end re-read the last live
+        // token (finite data) and are masked out of the softmax (P = 0).
+        const int kt_tok = min(col, live - 1);
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+          kr[m] = load_kv16v(kt + kt_tok * a.kv_ss + 8 * grp + 32 * m);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int tok = 4 * grp + r;
+          vr[r] = load_kv16v(vt + min(tok, live - 1) * a.kv_ss + 8 * col);
+          ok |= (unsigned)(tok < live) << r;
+        }
+      } else {
+        // K token tb + col; the V lanes fetch their tokens' slots from those lanes.
+        const int p = tb + col;
+        const int blk = block_of(p);
+        const int bid = __shfl(tbl, blk - cb);
+        const int64_t sl = (int64_t)bid * a.bs + (p - blk * a.bs);
+        const bool kon = p < t1 && sl >= 0 && sl < a.num_slots;
+        const int64_t kslot = kon ? sl : -1;
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+          kr[m] = kon ? load_kv16v(kbase + kslot * a.kv_ss + 8 * grp + 32 * m) : z;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int src = 4 * grp + r;
+          const int lo = __shfl((int)(kslot & 0xFFFFFFFF), src);
+          const int hi = __shfl((int)(kslot >> 32), src);
+          const int64_t vs = ((int64_t)hi << 32) | (uint32_t)lo;
+          const bool on = vs >= 0;
+          vr[r] = on ? load_kv16v(vbase + vs * a.kv_ss + 8 * col) : z;
+          ok |= (unsigned)on << r;
+        }
+      }
+      return ok;
+    };
+
+    float m_run = -INFINITY;  // running max of head column col (same in all 4 rows)
+    float l_run = 0.f;        // this row's share of the running sum
+    float acc[GPW][8];
+#pragma unroll
+    for (int g = 0; g < GPW; ++g)
+#pragma unroll
+      for (int d = 0; d < 8; ++d) acc[g][d] = 0.f;
+
+    auto tile = [&](const u32x4* kr, const u32x4* vr, unsigned ok) {
+      f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int m = 0; m < 4; ++m) s = MMA::mma(kr[m], qb[m], s);
+      float p[4];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        p[r] = ((ok >> r) & 1u) ? s[r] * a.scale_log2 : -INFINITY;
+        mx = fmaxf(mx, p[r]);
+      }
+      mx = rows_max(mx);
+      const float mn = fmaxf(m_run, mx);
+      const float mref = mn == -INFINITY ? 0.f : mn;  // all masked so far: stay at 0
+      const float alpha = __builtin_amdgcn_exp2f(m_run - mref);
+      m_run = mn;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) p[r] = __builtin_amdgcn_exp2f(p[r] - mref);
+      l_run = __builtin_fmaf(l_run, alpha, (p[0] + p[1]) + (p[2] + p[3]));
+      float vf[4][8];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) unpack16v<DT>(vr[r], vf[r]);
+#pragma unroll
+      for (int g = 0; g < GPW; ++g) {
+        const float al = row_bcast(alpha, g);
+#pragma unroll
+        for (int d = 0; d < 8; ++d) acc[g][d] *= al;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float pr = row_bcast(p[r], g);
+#pragma unroll
+          for (int d = 0; d < 8; ++d) acc[g][d] = __builtin_fmaf(pr, vf[r][d], acc[g][d]);
+        }
+      }
+    };
+
+    if (t0 < t1) {
+      load_table(block_of(t0));
+#if PKV_DECODE_PREFETCH >= 2
+      // Three tile buffers in rotation: two tiles in flight while one is reduced.
+      u32x4 k0[4], v0[4], k1[4], v1[4], k2[4], v2[4];
+      unsigned ok0 = load_tile(t0, k0, v0);
+      unsigned ok1 = load_tile(t0 + TILE, k1, v1);
+      unsigned ok2;
+      for (int tb = t0; tb < t1; tb += 3 * TILE) {
+        ok2 = load_tile(tb + 2 * TILE, k2, v2);
+        tile(k0, v0, ok0);
+        if (tb + TILE >= t1) break;
+        ok0 = load_tile(tb + 3 * TILE, k0, v0);
+        tile(k1, v1, ok1);
+        if (tb + 2 * TILE >= t1) break;
+        ok1 = load_tile(tb + 4 * TILE, k1, v1);
+        tile(k2, v2, ok2);
+      }
+#else
+      // Two tile buffers in ping-pong: the next tile is in flight while one is reduced.
+      u32x4 ka[4], va[4], kb2[4], vb2[4];
+      unsigned oka = load_tile(t0, ka, va);
+      for (int tb = t0; tb < t1; tb += 2 * TILE) {
+        const unsigned okb = load_tile(tb + TILE, kb2, vb2);
+        tile(ka, va, oka);
+        if (tb + TILE >= t1) break;
+        oka = load_tile(tb + 2 * TILE, ka, va);
+        tile(kb2, vb2, okb);
+      }
+#endif
+    }
+
+    // Totals: l over the four rows of each column, acc over the four rows.
+    const float l_tot = rows_sum(l_run);
+#pragma unroll
+    for (int g = 0; g < GPW; ++g)
+#pragma unroll
+      for (int d = 0; d < 8; ++d) acc[g][d] = rows_sum(acc[g][d]);
+    float lh[GPW], mh[GPW];
+#pragma unroll
+    for (int g = 0; g < GPW; ++g) {
+      lh[g] = row_bcast(l_tot, g);
+      mh[g] = row_bcast(m_run, g);
+    }
+
+    if (grp == 0) {  // lane c writes head dims 8c .. 8c + 7
+      const int d0 = 8 * col;
+      if (whole) {
+#pragma unroll
+        for (int g = 0; g < GPW; ++g) {
+          const float inv = lh[g] > 0.f ? 1.f / lh[g] : 0.f;
+          float o[8];
+#pragma unroll
+          for (int d = 0; d < 8; ++d) o[d] = acc[g][d] * inv;
+          const int64_t e = b * a.out_sb + (int64_t)(h0 + g) * a.out_sh + d0;
+          if (a.out_f32) store_vec<PKV_F32, 8>((float*)a.out + e, o);
+          else store_vec<DT, 8>((S*)a.out + e, o);
+        }
+      } else {
+#pragma unroll
+        for (int g = 0; g < GPW; ++g) {
+          const int64_t rec = ((int64_t)w * 2 + slot) * a.nh + h0 + g;
+          store_vec<PKV_F32, 8>(a.ws_acc + rec * HD + d0, acc[g]);
+          if (col == 0) *reinterpret_cast<float2*>(a.ws_ml + 2 * rec) = make_float2(mh[g], lh[g]);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// Combine pass: merges the pieces of sequences cut by a range boundary.
+//
+// Sequence b (units [ub, ue)) spans workgroups w0..w1; each non-empty range among them
+// holds one piece and wrote one record per query head (in w0 it is the range's last
+// piece, slot 1, unless the range starts with it). One wave per (sequence, query head)
+// merges them: out = sum_j w_j acc_j / sum_j w_j l_j with w_j = exp2(m_j - max m). The
+// sequence's merge plan (16 bytes written by the stream pass) says which records to
+// read; then one round trip per 16 records loads their (m, l) pairs and accumulator
+// rows together. Sequences that were not cut exit after reading the plan.
+// ---------------------------------------------------------------------------------
+
+// Total units, and the unit range [ub, ue) of sequence b, in one pass over the lengths.
+__device__ void seq_units(const DecodeArgs& a, int b, int64_t* ub, int64_t* ue, int64_t* total) {
+  const int lane = threadIdx.x & (kWave - 1);
+  int64_t before = 0, all = 0;
+  int mine = 0;
+  for (int c0 = 0; c0 < a.batch; c0 += kWave) {
+    const int bb = c0 + lane;
+    const int cnt = bb < a.batch ? units_of(a, clamped_ctx(a, bb)) : 0;
+    int lt = bb < b ? cnt : 0;
+    int tot = cnt;
+    if (bb == b) mine = cnt;
+#pragma unroll
+    for (int s = 1; s < kWave; s <<= 1) {
+      lt += __shfl_xor(lt, s);
+      tot += __shfl_xor(tot, s);
+    }
+    before += lt;
+    all += tot;
+  }
+#pragma unroll
+  for (int s = 1; s < kWave; s <<= 1) mine += __shfl_xor(mine, s);
+  *ub = before;
+  *ue = before + mine;
+  *total = all;
+}
+
+template <int DT, int HD>
 __global__ void __launch_bounds__(256)
-paged_decode_combine_kernel(const DecodeArgs a, int hd) {
+paged_decode_combine_kernel(const DecodeArgs a) {
+  constexpr int DPL = HD >= kWave ? HD / kWave : 1;  // head dims per lane
+  constexpr int kChunk = DPL >= 4 ? 16 : 32;          // records loaded per round trip
   const int lane = threadIdx.x & (kWave - 1);
   const int wid = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
   if (wid >= a.batch * a.nh) return;  // uniform per wave
   const int b = wid / a.nh, h = wid - b * a.nh;
 
-  int64_t total, ub;
-  find_unit(a, -1, &total);
-  // first unit of sequence b: the units of sequences before it
-  {
-    int64_t base = 0;
-    for (int c0 = 0; c0 < b; c0 += kWave) {
-      const int bb = c0 + lane;
-      int cnt = bb < b ? units_of(a, clamped_ctx(a, bb)) : 0;
-#pragma unroll
-      for (int m = 1; m < kWave; m <<= 1) cnt += __shfl_xor(cnt, m);
-      base += cnt;
-    }
-    ub = base;
-  }
-  const int64_t ue = ub + units_of(a, clamped_ctx(a, b));
-  const int64_t G = a.num_wg;
-  const int64_t w0 = wg_of_unit(ub, total, G), w1 = wg_of_unit(ue - 1, total, G);
-  if (w0 == w1) return;  // written directly by the split pass
-  const int nrec = (int)(w1 - w0 + 1);
+  const int4 plan = a.desc[b];
+  const int nrec = plan.y;
+  if (nrec <= 1) return;  // written directly by the stream pass
+  const int64_t w0 = plan.x;
+  // Units fewer than workgroups leave some ranges empty: then find the live ones.
+  int64_t ub = 0, ue = 0, total = 0;
+  if (!plan.w) seq_units(a, b, &ub, &ue, &total);
+  const int64_t row0 = (w0 * 2 + plan.z) * a.nh + h;  // record 0: always live
 
-  auto record = [&](int j, bool* live) -> int64_t {
-    const int64_t ww = w0 + j;
-    const int64_t s0 = range_start(ww, total, G);
-    *live = s0 < range_start(ww + 1, total, G);
-    const int slot = (ww == w0 && s0 < ub) ? 1 : 0;
-    return (ww * 2 + slot) * a.nh + h;
+  float out_acc[DPL], lsum = 0.f, mmax = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < DPL; ++k) out_acc[k] = 0.f;
+  // Fold records [j0, j0 + C) into the running (max, sum, acc). Every load is issued
+  // before any is used. Dead slots (past the last record, or an empty range) re-read
+  // record 0 -- finite data -- and get weight 0: records that were never written are
+  // not read, the scratch may hold NaN bit patterns.
+  auto fold = [&](auto chunk, int j0) {
+    constexpr int C = decltype(chunk)::value;
+    float m[C], l[C], x[C][DPL];
+#pragma unroll
+    for (int jj = 0; jj < C; ++jj) {
+      const int j = j0 + jj;
+      bool live = j < nrec;
+      if (!plan.w && live) {
+        const int64_t ww = w0 + j;
+        live = range_start(ww, total, a.num_wg) < range_start(ww + 1, total, a.num_wg);
+      }
+      const int64_t row = (live && j > 0) ? (w0 + j) * 2 * a.nh + h : row0;
+      const float2 ml = *reinterpret_cast<const float2*>(a.ws_ml + 2 * row);
+      m[jj] = live ? ml.x : -INFINITY;
+      l[jj] = ml.y;
+      const float* rowp = a.ws_acc + row * HD;
+#pragma unroll
+      for (int k = 0; k < DPL; ++k) x[jj][k] = (lane + kWave * k < HD) ? rowp[lane + kWave * k] : 0.f;
+    }
+    float mn = mmax;
+#pragma unroll
+    for (int jj = 0; jj < C; ++jj) mn = fmaxf(mn, m[jj]);
+    const float mref = mn == -INFINITY ? 0.f : mn;  // no live token yet: weights 0
+    const float alpha = __builtin_amdgcn_exp2f(mmax - mref);
+    mmax = mn;
+    lsum *= alpha;
+#pragma unroll
+    for (int k = 0; k < DPL; ++k) out_acc[k] *= alpha;
+#pragma unroll
+    for (int jj = 0; jj < C; ++jj) {
+      const float wj = __builtin_amdgcn_exp2f(m[jj] - mref);  // dead: exp2(-inf) = 0
+      lsum = __builtin_fmaf(wj, l[jj], lsum);
+#pragma unroll
+      for (int k = 0; k < DPL; ++k) out_acc[k] = __builtin_fmaf(wj, x[jj][k], out_acc[k]);
+    }
   };
-
-  float mmax = -INFINITY;
-  for (int j = lane; j < nrec; j += kWave) {
-    bool live;
-    const int64_t r = record(j, &live);
-    if (live) mmax = fmaxf(mmax, a.ws_ml[2 * r]);
+  if (nrec <= 8) {  // the common case: a sequence cut a few times
+    fold(std::integral_constant<int, 8>{}, 0);
+  } else {
+    for (int j0 = 0; j0 < nrec; j0 += kChunk) fold(std::integral_constant<int, kChunk>{}, j0);
   }
-#pragma unroll
-  for (int m = 1; m < kWave; m <<= 1) mmax = fmaxf(mmax, __shfl_xor(mmax, m));
-  if (mmax == -INFINITY) mmax = 0.f;  // no live token in any piece: weights 0, output 0
-
-  float out_acc[4] = {0.f, 0.f, 0.f, 0.f};  // dims lane + 64 k
-  float lsum = 0.f;
-  for (int c0 = 0; c0 < nrec; c0 += kWave) {
-    const int j = c0 + lane;
-    float wgt = 0.f;
-    int64_t r = 0;
-    if (j < nrec) {
-      bool live;
-      r = record(j, &live);
-      if (live) {
-        const float2 ml = *reinterpret_cast<const float2*>(a.ws_ml + 2 * r);
-        wgt = __builtin_amdgcn_exp2f(ml.x - mmax);
-        lsum = __builtin_fmaf(wgt, ml.y, lsum);
-      } else {
-        r = 0;
-      }
-    }
-    const int cn = min(kWave, nrec - c0);
-    for (int j0 = 0; j0 < cn; j0 += 8) {
-      float wv[8];
-      float x[8][4];
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj) {
-        const int src = min(j0 + jj, cn - 1);  // clamped duplicates get weight 0 below
-        wv[jj] = j0 + jj < cn
-                     ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wgt), src))
-                     : 0.f;
-        const int lo = __builtin_amdgcn_readlane((int)(r & 0xFFFFFFFF), src);
-        const int hi = __builtin_amdgcn_readlane((int)(r >> 32), src);
-        const int64_t rr = ((int64_t)hi << 32) | (uint32_t)lo;
-        const float* rowp = a.ws_acc + rr * hd;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          // rows of dead or duplicate records are never read: the workspace holds
-          // whatever the allocator left there, possibly NaN bit patterns
-          x[jj][k] = (wv[jj] != 0.f && lane + 64 * k < hd) ? rowp[lane + 64 * k] : 0.f;
-        }
-      }
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj) {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) out_acc[k] = __builtin_fmaf(wv[jj], x[jj][k], out_acc[k]);
-      }
-    }
-  }
-#pragma unroll
-  for (int m = 1; m < kWave; m <<= 1) lsum += __shfl_xor(lsum, m);
   const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int d = lane + 64 * k;
-    if (d >= hd) break;
+  for (int k = 0; k < DPL; ++k) {
+    const int d = lane + kWave * k;
+    if (d >= HD) break;
     const float o = out_acc[k] * inv;
     const int64_t e = b * a.out_sb + (int64_t)h * a.out_sh + d;
-    if constexpr (DTO == PKV_F32) reinterpret_cast<float*>(a.out)[e] = o;
-    else reinterpret_cast<typename Elt<DTO>::S*>(a.out)[e] = Elt<DTO>::from_f32(o);
+    if (a.out_f32) reinterpret_cast<float*>(a.out)[e] = o;
+    else reinterpret_cast<typename Elt<DT>::S*>(a.out)[e] = Elt<DT>::from_f32(o);
   }
 }
 
@@ -751,13 +1100,37 @@ template <class F> hipError_t by_dtype(int dt, int hd, int gpw, const F& f) {
   }
 }
 
+// The MFMA kernel serves 16-bit K/V at head_dim 128; every other shape uses the
+// generic stream kernel.
+template <int DT, int HD> constexpr bool use_mfma() {
+  return DT != PKV_F32 && HD == 128 && PKV_DECODE_USE_MFMA;
+}
+template <int DT, int HD, int GPW> const void* decode_kernel() {
+  if constexpr (use_mfma<DT, HD>())
+    return reinterpret_cast<const void*>(&paged_decode_mfma_kernel<DT, GPW, true>);
+  else
+    return reinterpret_cast<const void*>(&paged_decode_stream_kernel<DT, HD, GPW>);
+}
+
 struct LaunchDecode {
   const DecodeArgs* a;
   int wpg, ygrid;
   hipStream_t st;
   template <int DT, int HD, int GPW> hipError_t run() const {
-    hipLaunchKernelGGL((paged_decode_stream_kernel<DT, HD, GPW>),
-                       dim3((unsigned)a->num_wg, (unsigned)ygrid), dim3(kWave * wpg), 0, st, *a);
+    const dim3 grid((unsigned)a->num_wg, (unsigned)ygrid), block(kWave * wpg);
+    if constexpr (use_mfma<DT, HD>()) {
+      if (a->bs % 16 == 0)
+        hipLaunchKernelGGL((paged_decode_mfma_kernel<DT, GPW, true>), grid, block, 0, st, *a);
+      else
+        hipLaunchKernelGGL((paged_decode_mfma_kernel<DT, GPW, false>), grid, block, 0, st, *a);
+    } else {
+      hipLaunchKernelGGL((paged_decode_stream_kernel<DT, HD, GPW>), grid, block, 0, st, *a);
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || a->num_wg <= 1) return e;
+    const int waves = a->batch * a->nh;
+    hipLaunchKernelGGL((paged_decode_combine_kernel<DT, HD>), dim3((unsigned)((waves + 3) / 4)),
+                       dim3(256), 0, st, *a);
     return hipGetLastError();
   }
 };
@@ -771,9 +1144,8 @@ struct QueryDecode {
   template <int DT, int HD, int GPW> hipError_t run() const {
     *tile = DecodeShape<DT, HD>::TILE;
     if (!per_cu) return hipSuccess;
-    return hipOccupancyMaxActiveBlocksPerMultiprocessor(
-        per_cu, reinterpret_cast<const void*>(&paged_decode_stream_kernel<DT, HD, GPW>),
-        kWave * wpg, 0);
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, decode_kernel<DT, HD, GPW>(),
+                                                         kWave * wpg, 0);
   }
 };
 
@@ -920,11 +1292,12 @@ int32_t pkv_decode_workgroups(int kv_dtype, int32_t head_dim, int32_t num_heads,
   return g < 1 ? 1 : g;
 }
 
-int64_t pkv_decode_workspace_bytes(int32_t num_workgroups, int32_t num_heads,
+int64_t pkv_decode_workspace_bytes(int32_t num_workgroups, int32_t batch, int32_t num_heads,
                                    int32_t head_dim) {
-  if (num_workgroups <= 1 || num_heads <= 0 || head_dim <= 0) return 0;
+  if (num_workgroups <= 1 || batch <= 0 || num_heads <= 0 || head_dim <= 0) return 0;
   const int64_t recs = (int64_t)num_workgroups * 2 * num_heads;
-  return (recs * head_dim * 4 + 255) / 256 * 256 + recs * 2 * 4;
+  return ((int64_t)batch * 16 + 255) / 256 * 256 + (recs * head_dim * 4 + 255) / 256 * 256 +
+         recs * 2 * 4;
 }
 
 int pkv_paged_decode(void* out, int out_dtype, int64_t out_stride_b, int64_t out_stride_h,
@@ -982,36 +1355,22 @@ int pkv_paged_decode(void* out, int out_dtype, int64_t out_stride_b, int64_t out
   a.num_wg = num_workgroups;
   a.scale_log2 = scale * 1.4426950408889634f;
   a.out_f32 = out_dtype == PKV_F32;
+  a.desc = nullptr;
   a.ws_acc = nullptr;
   a.ws_ml = nullptr;
   if (num_workgroups > 1) {
-    const int64_t need = pkv_decode_workspace_bytes(num_workgroups, num_heads, head_dim);
+    const int64_t need = pkv_decode_workspace_bytes(num_workgroups, batch, num_heads, head_dim);
     if (!workspace || workspace_bytes < need || !aligned16(workspace)) return PKV_E_WORKSPACE;
     const int64_t recs = (int64_t)num_workgroups * 2 * num_heads;
-    a.ws_acc = (float*)workspace;
-    a.ws_ml = (float*)((char*)workspace + (recs * head_dim * 4 + 255) / 256 * 256);
+    char* p = (char*)workspace;
+    a.desc = (int4*)p;
+    p += ((int64_t)batch * 16 + 255) / 256 * 256;
+    a.ws_acc = (float*)p;
+    a.ws_ml = (float*)(p + (recs * head_dim * 4 + 255) / 256 * 256);
   }
 
   hipStream_t st = (hipStream_t)stream;
-  hipError_t e = by_dtype(kv_dtype, head_dim, p.gpw, LaunchDecode{&a, p.wpg, p.ygrid, st});
-  if (e != hipSuccess || num_workgroups <= 1) return (int)e;
-
-  const int waves = batch * num_heads;
-  const dim3 cgrid((unsigned)((waves + 3) / 4));
-  switch (out_dtype) {
-    case PKV_F32:
-      hipLaunchKernelGGL(paged_decode_combine_kernel<PKV_F32>, cgrid, dim3(256), 0, st, a,
-                         head_dim);
-      break;
-    case PKV_F16:
-      hipLaunchKernelGGL(paged_decode_combine_kernel<PKV_F16>, cgrid, dim3(256), 0, st, a,
-                         head_dim);
-      break;
-    default:
-      hipLaunchKernelGGL(paged_decode_combine_kernel<PKV_BF16>, cgrid, dim3(256), 0, st, a,
-                         head_dim);
-  }
-  return (int)hipGetLastError();
+  return (int)by_dtype(kv_dtype, head_dim, p.gpw, LaunchDecode{&a, p.wpg, p.ygrid, st});
 }
 
 }  // extern "C"

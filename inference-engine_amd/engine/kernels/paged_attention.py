@@ -6,10 +6,11 @@ lib/libpaged_kv.so:
 
 1. a stream-K pass: the contexts of all sequences, laid end to end, are split evenly
    over as many workgroups as the GPU holds at once. One wave per KV head streams its
-   share of K/V rows straight from the paged pool through the block table with
-   16-byte non-temporal loads, computes the scores of every query head sharing that KV
-   head (GQA: each K/V row is read once for the whole group), and keeps an fp32 online
-   softmax. Sequences that lie inside one workgroup's share are written directly.
+   share of K/V rows straight from the paged pool through the block table with 16-byte
+   non-temporal loads, computes the scores of every query head sharing that KV head
+   (GQA: each K/V row is read once for the whole group; on the matrix cores for 16-bit
+   caches at head_dim 128) and keeps an fp32 online softmax. Sequences inside one
+   workgroup's share are written directly.
 2. a combine pass that merges, with log-sum-exp weights, the pieces of the sequences
    cut by a share boundary.
 
@@ -73,6 +74,15 @@ def decode_workgroups(device: torch.device, dtype: torch.dtype, head_dim: int,
     return wgs
 
 
+def decode_workspace(device: torch.device, batch: int, num_heads: int, head_dim: int,
+                     num_workgroups: int) -> torch.Tensor | None:  # fmt: skip
+    """Scratch for ``paged_decode_attention(..., num_workgroups=n, workspace=)``, e.g. to
+    allocate it outside a hipGraph capture (None when the call needs none)."""
+    nbytes = _native.lib().pkv_decode_workspace_bytes(num_workgroups, batch, num_heads,
+                                                      head_dim)  # fmt: skip
+    return torch.empty(nbytes, dtype=torch.uint8, device=device) if nbytes else None
+
+
 def paged_decode_attention(
     q: torch.Tensor,
     k_cache: torch.Tensor,
@@ -84,6 +94,7 @@ def paged_decode_attention(
     *,
     out: torch.Tensor | None = None,
     num_workgroups: int | None = None,
+    workspace: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """q: [B, nh, hd]; k_cache, v_cache: [num_slots, nkv, hd] (one layer);
     block_tables: [B, max_blocks] int32; context_lens: [B] int32 -> [B, nh, hd].
@@ -92,7 +103,8 @@ def paged_decode_attention(
     Triton tile) is accepted and ignored. Extensions: ``out`` receives the result in
     place ([B, nh, hd], q.dtype or float32 for the unrounded fp32 result) and
     ``num_workgroups`` overrides how many workgroups share the contexts (default: as many
-    as the GPU holds at once).
+    as the GPU holds at once); ``workspace`` (uint8, from ``decode_workspace``) replaces
+    the scratch otherwise taken from torch's caching allocator on each call.
     """
     del block_n
     what = "paged_decode_attention"
@@ -136,8 +148,16 @@ def paged_decode_attention(
     if num_workgroups is None:
         num_workgroups = decode_workgroups(dev, q.dtype, hd, nh, nkv)
     lib = _native.lib()
-    ws_bytes = lib.pkv_decode_workspace_bytes(num_workgroups, nh, hd)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
+    ws_bytes = lib.pkv_decode_workspace_bytes(num_workgroups, b, nh, hd)
+    ws = None
+    if ws_bytes and workspace is not None:
+        if workspace.device != dev or workspace.dtype != torch.uint8 or \
+                workspace.numel() < ws_bytes or not workspace.is_contiguous():  # fmt: skip
+            raise ValueError(f"{what}: workspace must be a contiguous uint8 tensor of at "
+                             f"least {ws_bytes} bytes on {dev}")  # fmt: skip
+        ws = workspace
+    elif ws_bytes:
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     status = lib.pkv_paged_decode(
         out.data_ptr(), _native.dtype_code(out.dtype, what), out.stride(0), out.stride(1),
         q.data_ptr(), q.stride(0), q.stride(1),

@@ -46,9 +46,10 @@ def test_status_strings():
 
 def test_workspace_arithmetic():
     lib = _native.lib()
-    assert lib.pkv_decode_workspace_bytes(1, 24, 128) == 0
+    assert lib.pkv_decode_workspace_bytes(1, 64, 24, 128) == 0
     recs = 256 * 2 * 24
-    assert lib.pkv_decode_workspace_bytes(256, 24, 128) >= recs * (128 + 2) * 4
+    assert lib.pkv_decode_workspace_bytes(256, 64, 24, 128) >= 64 * 16 + recs * (128 + 2) * 4
+
     # without a GPU the device query fails cleanly
     if not torch.cuda.is_available():
         assert lib.pkv_decode_workgroups(2, 128, 24, 8) == -6

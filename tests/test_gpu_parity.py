@@ -320,10 +320,13 @@ def test_graph_capture_replay():
     nk_s = torch.zeros(b, nkv, hd, device=DEV, dtype=torch.bfloat16)
     nv_s = torch.zeros_like(nk_s)
     out_s = torch.empty(b, nh, hd, device=DEV, dtype=torch.bfloat16)
+    wgs = pa.decode_workgroups(DEV, torch.bfloat16, hd, nh, nkv)
+    ws = pa.decode_workspace(DEV, b, nh, hd, wgs)  # allocated outside the capture
 
     def body():
         kv_append(k_pool, v_pool, nk_s, nv_s, slots_s)
-        pa.paged_decode_attention(q_s, k_pool, v_pool, tables_s, ctx_s, bs, out=out_s)
+        pa.paged_decode_attention(q_s, k_pool, v_pool, tables_s, ctx_s, bs, out=out_s,
+                                  num_workgroups=wgs, workspace=ws)  # fmt: skip
 
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -353,6 +356,28 @@ def test_graph_capture_replay():
         torch.cuda.synchronize()
         assert torch.equal(_bits(got), _bits(want)), f"replay {rep}"
         assert torch.equal(_bits(k_pool[slots_s]), _bits(nk_s))
+
+
+@pytest.mark.parametrize("wgs", [7, 300])
+def test_workspace_reuse_and_garbage(wgs):
+    """The scratch may hold anything (here NaN bit patterns) and be reused across calls
+    of different shapes: results stay identical and match the oracle."""
+    _say("workspace reuse", wgs)
+    ws = pa.decode_workspace(DEV, 6, 32, 128, wgs)
+    ws.fill_(0xFF)  # 0xFFFFFFFF is a NaN
+    small = workloads.custom([3, 40], 32, 8, 128, 16, torch.bfloat16, DEV, seed=12)
+    step = workloads.custom([1, 700, 33, 2049, 16, 5000], 32, 8, 128, 16, torch.bfloat16,
+                            DEV, seed=11)  # fmt: skip
+    outs = []
+    for s_ in (step, small, step, small, step):
+        o = pa.paged_decode_attention(s_.q, s_.k_cache, s_.v_cache, s_.block_tables,
+                                      s_.context_lens, 16, num_workgroups=wgs, workspace=ws)  # fmt: skip
+        if s_ is step:
+            outs.append(o)
+    torch.cuda.synchronize()
+    for o in outs[1:]:
+        assert torch.equal(_bits(o), _bits(outs[0]))
+    _check_attention(step, wgs=wgs, what=f"ws{wgs}")
 
 
 def test_native_library_is_loaded_from_tree():
