@@ -112,6 +112,31 @@ int pkv_paged_decode(void* out, int out_dtype, int64_t out_stride_b, int64_t out
                      float scale, int32_t num_workgroups, void* workspace,
                      int64_t workspace_bytes, void* stream);
 
+/*
+ * Chunked-prefill attention over the paged pool, on the matrix cores. Replaces the
+ * reference's gather of each chunk's context slots plus FlashAttention varlen call
+ * (engine/model/layers.py:246-253, metadata from engine/runtime/paged_cache.py:159-202).
+ * Chunk c owns query tokens cu_seqlens_q[c] .. cu_seqlens_q[c+1]-1 of q and a context
+ * of n_c = clamp(context_lens[c], 0, max_blocks * block_size) tokens reached through
+ * block_tables row c, its own tokens last: query i of a chunk of q_c tokens sits at
+ * position n_c - q_c + i and attends to keys 0 .. n_c - q_c + i (bottom-right causal).
+ *   out[t, h] = softmax(scale * q[t,h] . K^T) V over those keys, KV head h / G.
+ * q, out: [tokens, num_heads, head_dim]; out in kv_dtype or PKV_F32. kv_dtype is bf16
+ * or fp16; head_dim in {32, 64, 128, 256}. max_query_len bounds every chunk's length
+ * (it sizes the grid, so one hipGraph capture serves every length up to it). Block ids
+ * must address the pool (out-of-range ids are clamped for memory safety only).
+ * Softmax statistics are fp32; for the P.V product the probabilities enter the matrix
+ * cores as fp16 (fp16 caches) or as a bf16 hi + lo pair (bf16 caches).
+ */
+int pkv_paged_prefill(void* out, int out_dtype, int64_t out_stride_tok, int64_t out_stride_h,
+                      const void* q, int64_t q_stride_tok, int64_t q_stride_h,
+                      const void* k_cache, const void* v_cache, int kv_dtype,
+                      int64_t kv_stride_slot, int64_t kv_stride_head, int64_t num_slots,
+                      const int32_t* block_tables, int64_t table_stride, int32_t max_blocks,
+                      const int32_t* context_lens, const int32_t* cu_seqlens_q, int32_t n_chunks,
+                      int32_t max_query_len, int32_t num_heads, int32_t num_kv_heads,
+                      int32_t head_dim, int32_t block_size, float scale, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1014,6 +1014,299 @@ paged_decode_combine_kernel(const DecodeArgs a) {
 }
 
 // ---------------------------------------------------------------------------------
+// Chunked-prefill attention on the matrix cores (16-bit K/V, head_dim 64/128/256).
+//
+// Chunk c has q_c query tokens (rows cu_q[c] .. cu_q[c+1] of q) and a context of n_c
+// tokens in the paged pool (its own tokens last): query i sits at position n_c - q_c + i
+// and attends to keys 0 .. n_c - q_c + i (bottom-right causal, as the reference's
+// PagedBatch._mixed / varlen path). For KV head g the query rows are (token, head j of
+// g's group) pairs, rho = token * G + j; a workgroup (4 waves) takes 128 of them, each
+// wave two 16-row tiles, and streams the context in 64-token key tiles:
+//   * K and V tiles are gathered from the pool with 16-byte loads into registers while
+//     the previous tile is being reduced, then stored to LDS with the 16-byte chunks of
+//     each token row XOR-swizzled by the token index (conflict-free operand reads).
+//   * S^T = K . Q^T with v_mfma_f32_16x16x32 (K rows from LDS as A, Q rows kept in
+//     VGPRs as B): lane (row n, grp g) gets keys 4g + r of each 16-key block for query
+//     row n.
+//   * fp32 online softmax per row (cross-row max/sum with permlane16/32 swaps).
+//   * O^T += V^T . P^T: P^T's fragment is the lane's own S^T values (the MFMA's
+//     contraction order over keys is chosen to match), so P needs no lane exchange;
+//     V^T comes from two ds_read_b64_tr_b16 transpose reads per MFMA. The rescale
+//     factor of row n lives in the lanes that hold O^T's row n.
+// P enters the second product in the K/V type; for bf16 as a hi + lo pair (fp32-like
+// accuracy), for fp16 rounded once.
+// ---------------------------------------------------------------------------------
+
+struct PrefillArgs {
+  void* out;
+  int64_t out_st, out_sh;
+  const void* q;
+  int64_t q_st, q_sh;
+  const void* k;
+  const void* v;
+  int64_t kv_ss, kv_sh, num_slots;
+  const int32_t* tables;
+  int64_t table_stride;
+  int32_t max_blocks;
+  const int32_t* ctx;   // [n_chunks] context tokens (the chunk's own included)
+  const int32_t* cu_q;  // [n_chunks + 1] query row offsets
+  int32_t n_chunks, nh, nkv, groups, bs, bs_shift;
+  int32_t row_blocks;   // grid.x: 128-row blocks per chunk (static bound)
+  float scale_log2;
+  int out_f32;
+};
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+template <int DT> struct Mfma16x16x32Bits;  // MFMA on raw 16-bit bit patterns
+template <> struct Mfma16x16x32Bits<PKV_BF16> {
+  typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+  __device__ static f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8, a),
+                                                   __builtin_bit_cast(v8, b), c, 0, 0, 0);
+  }
+  // two fp32 -> one dword of two bf16 (round to nearest even)
+  __device__ static uint32_t pack(float lo, float hi) {
+    return (uint32_t)Elt<PKV_BF16>::from_f32(lo) | ((uint32_t)Elt<PKV_BF16>::from_f32(hi) << 16);
+  }
+};
+template <> struct Mfma16x16x32Bits<PKV_F16> {
+  typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+  __device__ static f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8, a),
+                                                  __builtin_bit_cast(v8, b), c, 0, 0, 0);
+  }
+  __device__ static uint32_t pack(float lo, float hi) {
+    return (uint32_t)Elt<PKV_F16>::from_f32(lo) | ((uint32_t)Elt<PKV_F16>::from_f32(hi) << 16);
+  }
+};
+
+template <int DT, int HD>
+__global__ void __launch_bounds__(256)
+paged_prefill_kernel(const PrefillArgs a) {
+  constexpr int KT = 64;        // keys per tile
+  constexpr int CH = HD / 8;    // 16-byte chunks per K/V row
+  constexpr int KS = HD / 32;   // MFMA k-steps over head_dim
+  constexpr int DTL = HD / 16;  // 16-dim tiles of O^T
+  constexpr int NLD = KT * CH / 256;  // 16-byte loads per thread per tile, K and V each
+  static_assert(HD % 32 == 0 && HD <= 256, "head_dim must be 32..256, a multiple of 32");
+  using MMA = Mfma16x16x32Bits<DT>;
+  using S = typename Elt<DT>::S;
+  __shared__ __align__(16) u32x4 k_lds[KT * CH];
+  __shared__ __align__(16) u32x4 v_lds[KT * CH];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
+  const int col = lane & 15, grp = lane >> 4;
+  const int c = blockIdx.z, kvh = blockIdx.y;
+  const int q0 = a.cu_q[c], qlen = a.cu_q[c + 1] - q0;
+  const int G = a.groups;
+  const int nrows = qlen * G;
+  const int rho0 = blockIdx.x * 128;
+  if (qlen <= 0 || rho0 >= nrows) return;  // uniform per workgroup
+  const int cap = a.max_blocks * a.bs;
+  const int n = min(max(a.ctx[c], 0), cap);
+  const int base_pos = n - qlen;  // position of query token 0
+
+  // This lane's query row in each of its wave's two 16-row tiles (B operand column).
+  int row_tok[2];
+  bool row_ok[2];
+  u32x4 qf[2][KS];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int rho = rho0 + 32 * wave + 16 * t + col;
+    row_ok[t] = rho < nrows;
+    const int rr = row_ok[t] ? rho : 0;
+    row_tok[t] = rr / G;
+    const S* qp = reinterpret_cast<const S*>(a.q) + (int64_t)(q0 + row_tok[t]) * a.q_st +
+                  (int64_t)(kvh * G + rr % G) * a.q_sh + 8 * grp;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qf[t][s] = *reinterpret_cast<const u32x4*>(qp + 32 * s);
+  }
+  // Keys any row of this workgroup attends to: [0, kend).
+  const int last_row = min(nrows - 1, rho0 + 127);
+  const int kend = min(n, base_pos + last_row / G + 1);
+  const int ntiles = kend > 0 ? (kend + KT - 1) / KT : 0;
+
+  // Next tile's K/V in registers: thread tid fills LDS granules r * 256 + tid; granule
+  // (token t, position p) holds chunk p ^ (t % CH) of that token's row. Tokens past the
+  // context re-read the last context token (finite data, masked out of the softmax).
+  const int64_t tbl_row = (int64_t)c * a.table_stride;
+  u32x4 kst[NLD], vst[NLD];
+  auto fetch = [&](int kt0) {
+#pragma unroll
+    for (int r = 0; r < NLD; ++r) {
+      const int gi = r * 256 + tid;
+      const int t = gi / CH;
+      const int chunk = (gi % CH) ^ (t % CH);
+      const int p = min(kt0 + t, n - 1);
+      const int blk = a.bs_shift >= 0 ? (p >> a.bs_shift) : p / a.bs;
+      const int bid = a.tables[tbl_row + blk];
+      int64_t sl = (int64_t)bid * a.bs + (p - blk * a.bs);
+      sl = (sl >= 0 && sl < a.num_slots) ? sl : 0;
+      const int64_t off = sl * a.kv_ss + (int64_t)kvh * a.kv_sh + chunk * 8;
+      kst[r] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const S*>(a.k) + off);
+      vst[r] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const S*>(a.v) + off);
+    }
+  };
+  auto stash = [&]() {
+#pragma unroll
+    for (int r = 0; r < NLD; ++r) {
+      k_lds[r * 256 + tid] = kst[r];
+      v_lds[r * 256 + tid] = vst[r];
+    }
+  };
+
+  float m_run[2], l_run[2];
+  f32x4 o[2][DTL];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    m_run[t] = -INFINITY;
+    l_run[t] = 0.f;
+#pragma unroll
+    for (int d = 0; d < DTL; ++d) o[t][d] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  if (ntiles > 0) {
+    fetch(0);
+    stash();
+    __syncthreads();
+  }
+  for (int it = 0; it < ntiles; ++it) {
+    const int kt0 = it * KT;
+    if (it + 1 < ntiles) fetch(kt0 + KT);  // in flight while this tile is reduced
+
+    // S^T = K . Q^T: block beta holds keys 16 beta + 4 grp + r for query row col.
+    f32x4 sc[4][2];
+#pragma unroll
+    for (int beta = 0; beta < 4; ++beta) {
+      sc[beta][0] = sc[beta][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+      const int t = 16 * beta + col;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const u32x4 ka = k_lds[t * CH + ((4 * s + grp) ^ (t % CH))];
+        sc[beta][0] = MMA::mma(ka, qf[0][s], sc[beta][0]);
+        sc[beta][1] = MMA::mma(ka, qf[1][s], sc[beta][1]);
+      }
+    }
+
+    // Online softmax per query row; P^T fragments for the second product. bf16 keeps
+    // 8 significant bits, too few for P at the 2e-3 bar, so for bf16 P is also split
+    // into hi = bf16(P) and lo = bf16(P - hi) and both are multiplied into O.
+    constexpr bool kSplitP = DT == PKV_BF16;
+    u32x4 pb[2][2];  // [row tile][key half sigma]
+    u32x4 pl[2][2];  // low parts (kSplitP)
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int limit = min(n - 1, base_pos + row_tok[t]);  // last key this row sees
+      float p[4][4];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int beta = 0; beta < 4; ++beta)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int kpos = kt0 + 16 * beta + 4 * grp + r;
+          p[beta][r] = (row_ok[t] && kpos <= limit) ? sc[beta][t][r] * a.scale_log2 : -INFINITY;
+          mx = fmaxf(mx, p[beta][r]);
+        }
+      mx = rows_max(mx);
+      const float mn = fmaxf(m_run[t], mx);
+      const float mref = mn == -INFINITY ? 0.f : mn;
+      const float alpha = __builtin_amdgcn_exp2f(m_run[t] - mref);
+      m_run[t] = mn;
+      float psum = 0.f;
+#pragma unroll
+      for (int beta = 0; beta < 4; ++beta)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          p[beta][r] = __builtin_amdgcn_exp2f(p[beta][r] - mref);
+          psum += p[beta][r];
+        }
+      l_run[t] = __builtin_fmaf(l_run[t], alpha, psum);
+#pragma unroll
+      for (int d = 0; d < DTL; ++d) o[t][d] *= alpha;
+#pragma unroll
+      for (int sg = 0; sg < 2; ++sg) {
+        const float* a0 = p[2 * sg];
+        const float* a1 = p[2 * sg + 1];
+        pb[t][sg] = u32x4{MMA::pack(a0[0], a0[1]), MMA::pack(a0[2], a0[3]),
+                          MMA::pack(a1[0], a1[1]), MMA::pack(a1[2], a1[3])};
+        if constexpr (kSplitP) {
+          float r[8];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            r[e] = a0[e] - Elt<DT>::to_f32(Elt<DT>::from_f32(a0[e]));
+            r[4 + e] = a1[e] - Elt<DT>::to_f32(Elt<DT>::from_f32(a1[e]));
+          }
+          pl[t][sg] = u32x4{MMA::pack(r[0], r[1]), MMA::pack(r[2], r[3]),
+                            MMA::pack(r[4], r[5]), MMA::pack(r[6], r[7])};
+        }
+      }
+    }
+
+    // O^T += V^T . P^T. Lane col of group grp supplies token 32 sg + 4 grp + col / 4
+    // (+16 for the second read), dims 16 d + 4 (col % 4): the transpose read hands
+    // each lane 4 consecutive keys of one head dim.
+    char* vbytes = reinterpret_cast<char*>(v_lds);
+#pragma unroll
+    for (int sg = 0; sg < 2; ++sg) {
+#pragma unroll
+      for (int d = 0; d < DTL; ++d) {
+        u32x4 va;
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+          const int t = 32 * sg + 16 * h2 + 4 * grp + col / 4;
+          const int dim = 16 * d + 4 * (col % 4);
+          const int gran = t * CH + ((dim / 8) ^ (t % CH));
+          const int byte = gran * 16 + ((dim / 4) & 1) * 8;
+          // generic -> LDS address space (an addrspacecast of a __shared__ pointer)
+          const s16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vbytes + byte));
+          const uint32_t lo = (uint32_t)(uint16_t)x[0] | ((uint32_t)(uint16_t)x[1] << 16);
+          const uint32_t hi = (uint32_t)(uint16_t)x[2] | ((uint32_t)(uint16_t)x[3] << 16);
+          if (h2 == 0) { va.x = lo; va.y = hi; } else { va.z = lo; va.w = hi; }
+        }
+        o[0][d] = MMA::mma(va, pb[0][sg], o[0][d]);
+        o[1][d] = MMA::mma(va, pb[1][sg], o[1][d]);
+        if constexpr (kSplitP) {
+          o[0][d] = MMA::mma(va, pl[0][sg], o[0][d]);
+          o[1][d] = MMA::mma(va, pl[1][sg], o[1][d]);
+        }
+      }
+    }
+
+    if (it + 1 < ntiles) {
+      __syncthreads();  // every wave is done with this tile
+      stash();
+      __syncthreads();
+    }
+  }
+
+  // O^T lane (row col, grp) holds dims 16 d + 4 grp + r of query row col.
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const float l_tot = rows_sum(l_run[t]);
+    if (!row_ok[t]) continue;
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    const int rho = rho0 + 32 * wave + 16 * t + col;
+    const int64_t e0 = (int64_t)(q0 + rho / G) * a.out_st + (int64_t)(kvh * G + rho % G) * a.out_sh;
+#pragma unroll
+    for (int d = 0; d < DTL; ++d) {
+      const int64_t e = e0 + 16 * d + 4 * grp;
+      const float v4[4] = {o[t][d][0] * inv, o[t][d][1] * inv, o[t][d][2] * inv, o[t][d][3] * inv};
+      if (a.out_f32) {
+        *reinterpret_cast<float4*>((float*)a.out + e) = make_float4(v4[0], v4[1], v4[2], v4[3]);
+      } else {
+        *reinterpret_cast<uint2*>((S*)a.out + e) =
+            make_uint2((uint32_t)Elt<DT>::from_f32(v4[0]) | ((uint32_t)Elt<DT>::from_f32(v4[1]) << 16),
+                       (uint32_t)Elt<DT>::from_f32(v4[2]) | ((uint32_t)Elt<DT>::from_f32(v4[3]) << 16));
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------
 // Host-side dispatch.
 // ---------------------------------------------------------------------------------
 
@@ -1184,6 +1477,19 @@ int check_decode_shape(int kv_dtype, int head_dim, int num_heads, int num_kv_hea
         head_dim == 256))
     return PKV_E_SHAPE;
   return 0;
+}
+
+
+template <int DT>
+hipError_t launch_prefill(const PrefillArgs& a, int hd, hipStream_t st) {
+  const dim3 grid((unsigned)a.row_blocks, (unsigned)a.nkv, (unsigned)a.n_chunks), block(256);
+  switch (hd) {
+    case 32: hipLaunchKernelGGL((paged_prefill_kernel<DT, 32>), grid, block, 0, st, a); break;
+    case 64: hipLaunchKernelGGL((paged_prefill_kernel<DT, 64>), grid, block, 0, st, a); break;
+    case 128: hipLaunchKernelGGL((paged_prefill_kernel<DT, 128>), grid, block, 0, st, a); break;
+    default: hipLaunchKernelGGL((paged_prefill_kernel<DT, 256>), grid, block, 0, st, a);
+  }
+  return hipGetLastError();
 }
 
 }  // namespace
@@ -1371,6 +1677,63 @@ int pkv_paged_decode(void* out, int out_dtype, int64_t out_stride_b, int64_t out
 
   hipStream_t st = (hipStream_t)stream;
   return (int)by_dtype(kv_dtype, head_dim, p.gpw, LaunchDecode{&a, p.wpg, p.ygrid, st});
+}
+
+int pkv_paged_prefill(void* out, int out_dtype, int64_t out_stride_tok, int64_t out_stride_h,
+                      const void* q, int64_t q_stride_tok, int64_t q_stride_h,
+                      const void* k_cache, const void* v_cache, int kv_dtype,
+                      int64_t kv_stride_slot, int64_t kv_stride_head, int64_t num_slots,
+                      const int32_t* block_tables, int64_t table_stride, int32_t max_blocks,
+                      const int32_t* context_lens, const int32_t* cu_seqlens_q, int32_t n_chunks,
+                      int32_t max_query_len, int32_t num_heads, int32_t num_kv_heads,
+                      int32_t head_dim, int32_t block_size, float scale, void* stream) {
+  if (!(kv_dtype == PKV_BF16 || kv_dtype == PKV_F16)) return PKV_E_DTYPE;
+  if (!(out_dtype == kv_dtype || out_dtype == PKV_F32)) return PKV_E_DTYPE;
+  if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads || block_size <= 0 ||
+      max_blocks < 0 || n_chunks < 0 || n_chunks > 65535 || max_query_len < 0 ||
+      num_kv_heads > 65535)
+    return PKV_E_SHAPE;
+  if (!(head_dim == 32 || head_dim == 64 || head_dim == 128 || head_dim == 256)) return PKV_E_SHAPE;
+  if ((int64_t)max_blocks * block_size > (int64_t)1 << 30) return PKV_E_SHAPE;
+  const int64_t rows = (int64_t)max_query_len * (num_heads / num_kv_heads);
+  if (rows > (int64_t)1 << 30) return PKV_E_SHAPE;
+  if (n_chunks == 0 || max_query_len == 0) return 0;
+  if (!out || !q || !k_cache || !v_cache || !context_lens || !cu_seqlens_q ||
+      (max_blocks > 0 && !block_tables))
+    return PKV_E_NULL;
+  if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out) ||
+      q_stride_tok % 8 || q_stride_h % 8 || kv_stride_slot % 8 || kv_stride_head % 8 ||
+      out_stride_tok % 8 || out_stride_h % 8)
+    return PKV_E_ALIGN;
+  PrefillArgs a;
+  a.out = out;
+  a.out_st = out_stride_tok;
+  a.out_sh = out_stride_h;
+  a.q = q;
+  a.q_st = q_stride_tok;
+  a.q_sh = q_stride_h;
+  a.k = k_cache;
+  a.v = v_cache;
+  a.kv_ss = kv_stride_slot;
+  a.kv_sh = kv_stride_head;
+  a.num_slots = num_slots;
+  a.tables = block_tables;
+  a.table_stride = table_stride;
+  a.max_blocks = max_blocks;
+  a.ctx = context_lens;
+  a.cu_q = cu_seqlens_q;
+  a.n_chunks = n_chunks;
+  a.nh = num_heads;
+  a.nkv = num_kv_heads;
+  a.groups = num_heads / num_kv_heads;
+  a.bs = block_size;
+  a.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz(block_size) : -1;
+  a.row_blocks = (int)((rows + 127) / 128);
+  a.scale_log2 = scale * 1.4426950408889634f;
+  a.out_f32 = out_dtype == PKV_F32;
+  hipStream_t st = (hipStream_t)stream;
+  return (int)(kv_dtype == PKV_BF16 ? launch_prefill<PKV_BF16>(a, head_dim, st)
+                                    : launch_prefill<PKV_F16>(a, head_dim, st));
 }
 
 }  // extern "C"

@@ -45,6 +45,15 @@ SIGNATURES: dict[str, tuple] = {
          _p, _i32, _i32, _i32, _i32, _i32,        # ctx, batch, nh, nkv, hd, bs
          _f32, _i32, _p, _i64, _p],               # scale, wgs, workspace, stream
     ),  # fmt: skip
+    "pkv_paged_prefill": (
+        ctypes.c_int,
+        [_p, ctypes.c_int, _i64, _i64,            # out
+         _p, _i64, _i64,                          # q
+         _p, _p, ctypes.c_int, _i64, _i64, _i64,  # k, v caches
+         _p, _i64, _i32,                          # block tables
+         _p, _p, _i32, _i32,                      # ctx, cu_q, n_chunks, max_query_len
+         _i32, _i32, _i32, _i32, _f32, _p],       # nh, nkv, hd, bs, scale, stream
+    ),  # fmt: skip
 }
 
 _lib: ctypes.CDLL | None = None

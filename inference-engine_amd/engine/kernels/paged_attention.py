@@ -194,3 +194,80 @@ def reference_decode_attention(
         w = torch.softmax((k @ q[i].float()[:, :, None])[..., 0] * scale, dim=-1)  # [nh, n]
         outs.append((w[:, None, :] @ v)[:, 0])  # [nh, hd]
     return torch.stack(outs).to(q.dtype)
+
+
+PREFILL_HEAD_DIMS = (32, 64, 128, 256)
+
+
+def paged_prefill_attention(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    context_lens: torch.Tensor,
+    block_size: int,
+    cu_seqlens_q: torch.Tensor,
+    max_query_len: int,
+    *,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Bottom-right causal attention of prompt chunks over the paged pool (MFMA).
+
+    q: [T, nh, hd] -- the query tokens of all chunks back to back; chunk c owns rows
+    cu_seqlens_q[c] .. cu_seqlens_q[c+1]-1. block_tables: int32 [C, W];
+    context_lens: int32 [C], tokens in the cache for chunk c including its own (which
+    come last). Query i of a chunk of q_c tokens attends to keys 0 .. ctx_c - q_c + i.
+    -> [T, nh, hd] in q.dtype (or ``out``, q.dtype or float32).
+
+    Replaces the gather of every chunk's context slots plus the FlashAttention varlen call
+    of the reference (engine/model/layers.py:246-253; metadata built at
+    engine/runtime/paged_cache.py:182-202) without materialising the gathered K/V.
+    ``max_query_len`` bounds every chunk (it sizes the grid: one graph per bucket).
+    """
+    what = "paged_prefill_attention"
+    dev = _native.require_gpu(what, q, k_cache, v_cache, block_tables, context_lens,
+                              cu_seqlens_q)  # fmt: skip
+    if q.dim() != 3 or k_cache.dim() != 3 or v_cache.shape != k_cache.shape:
+        raise ValueError(f"{what}: q [T, nh, hd] and equal caches [slots, nkv, hd] expected")
+    t, nh, hd = q.shape
+    nkv = k_cache.shape[1]
+    if k_cache.shape[2] != hd or nh % nkv:
+        raise ValueError(f"{what}: cache {tuple(k_cache.shape)} does not fit q {tuple(q.shape)}")
+    if hd not in PREFILL_HEAD_DIMS:
+        raise ValueError(f"{what}: head_dim {hd} not in {PREFILL_HEAD_DIMS}")
+    if q.dtype not in (torch.bfloat16, torch.float16) or k_cache.dtype != q.dtype or \
+            v_cache.dtype != q.dtype:  # fmt: skip
+        raise TypeError(f"{what}: q and caches must share one dtype, bfloat16 or float16")
+    if k_cache.stride() != v_cache.stride() or k_cache.stride(2) != 1:
+        raise ValueError(f"{what}: k_cache and v_cache need equal strides, unit in head_dim")
+    for name, x in (("block_tables", block_tables), ("context_lens", context_lens),
+                    ("cu_seqlens_q", cu_seqlens_q)):  # fmt: skip
+        if x.dtype != torch.int32:
+            raise TypeError(f"{what}: {name} must be int32")
+    n_chunks = context_lens.numel()
+    if block_tables.dim() != 2 or block_tables.shape[0] != n_chunks or \
+            block_tables.stride(1) != 1 or cu_seqlens_q.shape != (n_chunks + 1,):  # fmt: skip
+        raise ValueError(f"{what}: block_tables [C, W], context_lens [C], cu_seqlens_q [C+1]")
+    q = q.contiguous()
+    if out is None:
+        out = torch.empty_like(q)
+    elif out.shape != q.shape or out.dtype not in (q.dtype, torch.float32) or \
+            out.stride(2) != 1 or out.device != dev:  # fmt: skip
+        raise ValueError(f"{what}: out must be [T, nh, hd] of {q.dtype} or float32 on {dev}")
+    if block_size <= 0:
+        raise ValueError(f"{what}: block_size must be positive")
+    if n_chunks == 0 or t == 0:
+        return out
+    context_lens = context_lens.contiguous()
+    cu_seqlens_q = cu_seqlens_q.contiguous()
+    status = _native.lib().pkv_paged_prefill(
+        out.data_ptr(), _native.dtype_code(out.dtype, what), out.stride(0), out.stride(1),
+        q.data_ptr(), q.stride(0), q.stride(1),
+        k_cache.data_ptr(), v_cache.data_ptr(), _native.dtype_code(k_cache.dtype, what),
+        k_cache.stride(0), k_cache.stride(1), k_cache.shape[0],
+        block_tables.data_ptr(), block_tables.stride(0), block_tables.shape[1],
+        context_lens.data_ptr(), cu_seqlens_q.data_ptr(), n_chunks, int(max_query_len),
+        nh, nkv, hd, block_size, hd**-0.5, _native.stream_of(dev),
+    )  # fmt: skip
+    _native.check(status, what)
+    return out

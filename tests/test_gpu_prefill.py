@@ -1,0 +1,133 @@
+"""Parity of the MFMA chunked-prefill kernel (through the C ABI) with the CPU oracle's
+bottom-right causal chunk attention (the semantics of the reference's PagedBatch._mixed
+and Attention._mixed, engine/runtime/paged_cache.py:182-194, engine/model/layers.py:
+246-265). The fp32 result must be within max-abs 2e-3 of the oracle; the q.dtype result
+equals that fp32 result rounded by torch."""
+
+from __future__ import annotations
+
+import os
+
+import pytest
+import torch
+
+from engine.kernels import paged_attention as pa
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+THREADS = min(16, os.cpu_count() or 1)
+ATOL = 2e-3
+
+
+def _say(*a):
+    print("[case]", *a, flush=True)
+
+
+def _bits(t):
+    return t.view(torch.uint8)
+
+
+def _chunks(spec, nh, nkv, hd, bs, dtype, seed, extra_blocks=5):
+    """spec: [(new tokens q_c, context n_c)], tables scattered over a shared pool."""
+    g = torch.Generator().manual_seed(seed)
+    nblk = sum(-(-n // bs) for _, n in spec) + extra_blocks
+    perm = torch.randperm(nblk, generator=g)
+    width = max(-(-n // bs) for _, n in spec)
+    tables = torch.zeros(len(spec), width, dtype=torch.int32)
+    at = 0
+    for i, (_, n) in enumerate(spec):
+        nb = -(-n // bs)
+        tables[i, :nb] = perm[at : at + nb].int()
+        at += nb
+    k = torch.randn(nblk * bs, nkv, hd, generator=g).to(dtype)
+    v = torch.randn(nblk * bs, nkv, hd, generator=g).to(dtype)
+    qlens = [q for q, _ in spec]
+    cu = torch.tensor([0, *torch.tensor(qlens).cumsum(0).tolist()], dtype=torch.int32)
+    q = torch.randn(int(cu[-1]), nh, hd, generator=g).to(dtype)
+    ctx = torch.tensor([n for _, n in spec], dtype=torch.int32)
+    return q, k, v, tables, ctx, cu
+
+
+def _run(q, k, v, tables, ctx, cu, bs, max_q):
+    args = (q.to(DEV), k.to(DEV), v.to(DEV), tables.to(DEV), ctx.to(DEV), bs, cu.to(DEV), max_q)
+    out32 = torch.empty(q.shape, dtype=torch.float32, device=DEV)
+    pa.paged_prefill_attention(*args, out=out32)
+    outq = pa.paged_prefill_attention(*args)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(outq), _bits(out32.to(q.dtype))), "rounding of the fp32 result"
+    return out32.cpu()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize(("nh", "nkv", "hd"), [(8, 2, 64), (4, 2, 128), (24, 8, 128), (6, 2, 32)])
+def test_prefill_reference_varlen_spec(dtype, nh, nkv, hd):
+    """The reference's own mixed-step spec (tests/test_kernels.py:199), block size 4."""
+    _say("prefill varlen spec", dtype, nh, nkv, hd)
+    spec = [(1, 9), (6, 6), (1, 3), (5, 13), (3, 20), (1, 1)]
+    q, k, v, tables, ctx, cu = _chunks(spec, nh, nkv, hd, 4, dtype, seed=0)
+    got = _run(q, k, v, tables, ctx, cu, 4, max(s for s, _ in spec))
+    want = oracle.prefill_attention(q, k, v, tables, cu, ctx, 4, threads=THREADS)
+    err = (got - want).abs().max().item()
+    assert err <= ATOL, err
+
+
+@pytest.mark.parametrize(("nh", "nkv"), [(32, 8), (24, 8), (8, 8), (16, 1)])
+@pytest.mark.parametrize("bs", [16, 1, 8])
+def test_prefill_groups_and_block_sizes(nh, nkv, bs):
+    _say("prefill groups/bs", nh, nkv, bs)
+    spec = [(70, 70), (33, 200), (128, 129), (1, 77), (200, 450)]
+    q, k, v, tables, ctx, cu = _chunks(spec, nh, nkv, 128, bs, torch.bfloat16, seed=nh + bs)
+    got = _run(q, k, v, tables, ctx, cu, bs, 200)
+    want = oracle.prefill_attention(q, k, v, tables, cu, ctx, bs, threads=THREADS)
+    assert (got - want).abs().max().item() <= ATOL
+
+
+def test_prefill_config5_chunks_first_and_last_tokens():
+    """Config 5's prompt chunks (Llama-3-8B shape): 4 chunks of 512 tokens after cached
+    prefixes of 0, 1024, 2048, 3072 tokens. The oracle checks each chunk's first and
+    last 16 query tokens (as their own sub-chunks with the same visible keys)."""
+    _say("prefill config5")
+    bs, nh, nkv, hd = 16, 32, 8, 128
+    spec = [(512, 512 + 1024 * i) for i in range(4)]
+    q, k, v, tables, ctx, cu = _chunks(spec, nh, nkv, hd, bs, torch.bfloat16, seed=5)
+    got = _run(q, k, v, tables, ctx, cu, bs, 512)
+    for part in ("first", "last"):
+        rows, sub_ctx, sub_cu = [], [], [0]
+        for c, (ql, n) in enumerate(spec):
+            start = int(cu[c]) + (0 if part == "first" else ql - 16)
+            rows.append(torch.arange(start, start + 16))
+            # the first 16 queries see keys up to n - ql + 15: a context of n - ql + 16
+            sub_ctx.append(n - ql + 16 if part == "first" else n)
+            sub_cu.append(sub_cu[-1] + 16)
+        rows = torch.cat(rows)
+        want = oracle.prefill_attention(q[rows], k, v, tables, torch.tensor(sub_cu, dtype=torch.int32),
+                                        torch.tensor(sub_ctx, dtype=torch.int32), bs,
+                                        threads=THREADS)  # fmt: skip
+        err = (got[rows] - want).abs().max().item()
+        assert err <= ATOL, (part, err)
+
+
+def test_prefill_whole_prompt_is_causal_attention():
+    """A chunk with no cached prefix (ctx == q) is plain causal attention: torch SDPA
+    with is_causal=True, computed here in float32 on the gathered rows."""
+    _say("prefill causal")
+    bs, nh, nkv, hd = 16, 8, 2, 128
+    q, k, v, tables, ctx, cu = _chunks([(300, 300)], nh, nkv, hd, bs, torch.bfloat16, seed=9)
+    got = _run(q, k, v, tables, ctx, cu, bs, 300)
+    slots = (tables[0, torch.arange(300) // bs].long() * bs + torch.arange(300) % bs)
+    kk = k[slots].float().permute(1, 0, 2).repeat_interleave(nh // nkv, 0)
+    vv = v[slots].float().permute(1, 0, 2).repeat_interleave(nh // nkv, 0)
+    want = torch.nn.functional.scaled_dot_product_attention(
+        q.float().permute(1, 0, 2), kk, vv, is_causal=True).permute(1, 0, 2)
+    assert (got - want).abs().max().item() <= ATOL
+
+
+def test_prefill_grid_bound_and_empty_chunks():
+    """max_query_len larger than every chunk (a graph bucket), and zero-length chunks."""
+    _say("prefill bounds")
+    spec = [(0, 10), (5, 5), (0, 0), (17, 40)]
+    q, k, v, tables, ctx, cu = _chunks(spec, 8, 2, 64, 4, torch.bfloat16, seed=3)
+    got = _run(q, k, v, tables, ctx, cu, 4, 256)
+    want = oracle.prefill_attention(q, k, v, tables, cu, ctx, 4, threads=THREADS)
+    assert (got - want).abs().max().item() <= ATOL
