@@ -1,17 +1,24 @@
-"""Benchmark of the paged decode attention hot path on one MI355X.
+"""Benchmark of the paged-KV hot path on one MI355X.
 
     python bench.py [--steps K] [--warmup W] [--config c2] [--layers L]
 
-A step is one layer-step of paged decode attention (stream-K pass + combine) over the
-config's batch, on cuda:0. L independent layer pools (default 4, ~1 GB each at config 2)
-are used in rotation, so every step reads K/V that the previous step did not touch,
-as consecutive layers of a model do; the 256 MB last-level cache cannot serve them.
-Timing: torch.cuda.Event pairs around every launch on torch's current stream, which is
-the stream the library launches on; the timed region is bracketed by synchronize().
+Default workload (BASELINE.json's metric): config 2, a Llama-3.2-3B decode step (B=64,
+contexts U[1024, 4096], 24 q / 8 KV heads, hd 128, bf16, 16-token blocks). A step is one
+layer-step of paged decode attention (stream-K pass + combine) over the batch on cuda:0.
+L independent layer pools (default 4, ~1 GB each at config 2) are used in rotation, so
+every step reads K/V the previous step did not touch, as consecutive layers of a model
+do; the 256 MB last-level cache cannot serve them.
 
-Prints one JSON line: value = mean microseconds per layer-step of decode attention;
-roofline.achieved = algorithmic K+V bytes (sum(ctx) * 2 * nkv * hd * 2 B) / the mean
-launch duration. cpu_baseline times the C oracle on the same config on host cores.
+Timing. ``value`` is the mean time per layer-step when the L layer-steps are captured in
+one hipGraph and replayed (the reference runs decode steps as CUDA-graph replays,
+engine/runtime/cuda_graphs.py), between events bracketed by synchronize(). ``eager_us``
+is the mean of per-call events around eager calls (includes per-call launch costs).
+``roofline.achieved`` = algorithmic K+V bytes (sum(ctx) * 2 * nkv * hd * 2 B) / the
+graph-replay time per layer-step. ``cpu_baseline`` times the C oracle on host cores.
+
+``--config c5`` measures the mixed chunked-prefill step of config 5 instead (append of
+2,168 rows, MFMA prefill of 4 x 512-token chunks, decode of 120 sequences); its line
+reports the prefill's TFLOP/s against the bf16 MFMA peak.
 """
 
 from __future__ import annotations
@@ -28,7 +35,9 @@ sys.path.insert(0, ROOT)
 sys.path.insert(0, os.path.join(ROOT, "inference-engine_amd"))
 
 HBM_PEAK_GBPS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_traffic.json")
+METRIC = "paged decode attn us/layer-step + achieved HBM GB/s (% of 8 TB/s), 3B shape"
 
 
 def parse() -> argparse.Namespace:
@@ -36,10 +45,11 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4"])
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
     ap.add_argument("--layers", type=int, default=4)
     ap.add_argument("--workgroups", type=int, default=None)
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-graph", action="store_true", help="time eager calls only")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--copy-calibration", action="store_true",
@@ -76,15 +86,50 @@ def cpu_baseline(step, budget_s: float) -> dict:
     }  # fmt: skip
 
 
-def main() -> int:
-    args = parse()
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build measures one GPU only (the decode path has no "
-              "cross-GPU exchange on one box); run with --gpus 1", file=sys.stderr)  # fmt: skip
-        return 2
+def eager_us(torch, fns, steps: int, warmup: int) -> list[float]:
+    """Per-call event times (µs) of fns called round-robin."""
+    for i in range(warmup):
+        fns[i % len(fns)]()
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]  # fmt: skip
+    for i, (a, z) in enumerate(ev):
+        a.record()
+        fns[i % len(fns)]()
+        z.record()
+    torch.cuda.synchronize()
+    return [a.elapsed_time(z) * 1e3 for a, z in ev]
 
-    import torch
 
+def graph_us(torch, fns, steps: int, warmup: int) -> tuple[float, float]:
+    """Capture fns (one pass) in a hipGraph and replay it until `steps` calls ran.
+    Returns (µs per call -- per element of fns, wall seconds of the timed region)."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for f in fns:
+            f()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for f in fns:
+            f()
+    for _ in range(max(1, warmup // len(fns))):
+        graph.replay()
+    reps = max(1, steps // len(fns))
+    torch.cuda.synchronize()
+    a, z = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    a.record()
+    for _ in range(reps):
+        graph.replay()
+    z.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return a.elapsed_time(z) * 1e3 / (reps * len(fns)), wall
+
+
+def bench_decode(args, torch) -> dict:
     from engine import workloads
     from engine.kernels import paged_attention as pa
     from engine.runtime.paged_cache import copy_blocks, kv_append
@@ -103,55 +148,43 @@ def main() -> int:
     wgs = args.workgroups or pa.decode_workgroups(dev, step.q.dtype, hd, nh, nkv)
     out = torch.empty_like(step.q)
 
-    def attn(i: int) -> None:
-        k, v = pools[i % len(pools)]
-        pa.paged_decode_attention(step.q, k, v, step.block_tables, step.context_lens,
-                                  step.block_size, out=out, num_workgroups=wgs)  # fmt: skip
+    def attn_fn(k, v):
+        return lambda: pa.paged_decode_attention(
+            step.q, k, v, step.block_tables, step.context_lens, step.block_size, out=out,
+            num_workgroups=wgs)  # fmt: skip
 
-    for i in range(args.warmup):
-        attn(i)
-    torch.cuda.synchronize()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(args.steps)]  # fmt: skip
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        ev[i][0].record()
-        attn(i)
-        ev[i][1].record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    per = [a.elapsed_time(z) * 1e3 for a, z in ev]  # microseconds
-    mean_us = statistics.fmean(per)
+    fns = [attn_fn(k, v) for k, v in pools]
+    per = eager_us(torch, fns, args.steps, args.warmup)
+    eager_mean = statistics.fmean(per)
+    if args.no_graph:
+        value, wall = eager_mean, None
+    else:
+        value, wall = graph_us(torch, fns, args.steps, args.warmup)
 
-    # KV append of the same batch (one layer), timed the same way.
-    ap_ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-             for _ in range(50)]  # fmt: skip
-    for a, z in ap_ev:
-        a.record()
+    def append():
         kv_append(step.k_cache, step.v_cache, step.new_k, step.new_v, step.slot_mapping)
-        z.record()
-    torch.cuda.synchronize()
-    append_us = statistics.fmean(a.elapsed_time(z) * 1e3 for a, z in ap_ev)
+
+    append_us = graph_us(torch, [append] * 8, 400, 16)[0]
 
     kv_bytes = step.kv_bytes()
-    gbps = kv_bytes / (mean_us * 1e-6) / 1e9
+    gbps = kv_bytes / (value * 1e-6) / 1e9
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
-            traffic = json.load(f).get(step.name)
+            traffic = (json.load(f).get(step.name) or {}).get("bytes")
     line = {
-        "metric": "paged decode attn us/layer-step + achieved HBM GB/s (% of 8 TB/s), 3B shape",
-        "value": round(mean_us, 2),
+        "metric": METRIC,
+        "value": round(value, 2),
         "unit": "us/layer-step",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(wall * 1e3 / args.steps, 4),
+        "ms_per_step": round(value / 1e3, 5),
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16" if step.q.dtype == torch.bfloat16 else str(step.q.dtype).split(".")[-1],
-        "data": "synthetic (seeded N(0,1) pools, queries; scattered block tables)",
+        "data": "synthetic (seeded N(0,1) pools and queries; scattered block tables)",
         "config": {
             "workload": step.name,
             "batch": b,
@@ -163,6 +196,7 @@ def main() -> int:
             "sum_ctx": int(step.context_lens.sum()),
             "workgroups": wgs,
             "layer_pools": len(pools),
+            "timing": "eager" if args.no_graph else "hipgraph replay",
         },
         "roofline": {
             "bound": "hbm",
@@ -173,18 +207,104 @@ def main() -> int:
             "traffic": traffic,
         },
         "kv_bytes_per_step": kv_bytes,
-        "median_us": round(statistics.median(per), 2),
+        "eager_us": round(eager_mean, 2),
+        "eager_median_us": round(statistics.median(per), 2),
         "append_us": round(append_us, 2),
     }
+    if wall is not None:
+        line["timed_wall_s"] = round(wall, 4)
+    if step.cow_mapping is not None:
+        line["unique_kv_bytes_per_step"] = step.unique_kv_bytes()
+        line["unique_gbps"] = round(line["unique_kv_bytes_per_step"] / (value * 1e-6) / 1e9, 1)
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(step, args.cpu_seconds)
+    return line
+
+
+def bench_mixed(args, torch) -> dict:
+    from engine import workloads
+    from engine.kernels import paged_attention as pa
+    from engine.runtime.paged_cache import kv_append
+
+    dev = torch.device("cuda:0")
+    m = workloads.config5(dev, seed=args.seed)
+    d = m.decode
+    out_c = torch.empty_like(m.q_chunks)
+    out_d = torch.empty_like(d.q)
+    nh, hd = d.q.shape[1], d.q.shape[2]
+    wgs = args.workgroups or pa.decode_workgroups(dev, d.q.dtype, hd, nh, d.k_cache.shape[1])
+
+    def append():
+        kv_append(m.k_cache, m.v_cache, m.new_k, m.new_v, m.slot_mapping)
+
+    def prefill():
+        pa.paged_prefill_attention(m.q_chunks, m.k_cache, m.v_cache, m.chunk_tables,
+                                   m.chunk_ctx, m.block_size, m.cu_q, m.max_query_len,
+                                   out=out_c)  # fmt: skip
+
+    def decode():
+        pa.paged_decode_attention(d.q, d.k_cache, d.v_cache, d.block_tables, d.context_lens,
+                                  d.block_size, out=out_d, num_workgroups=wgs)  # fmt: skip
+
+    append()
+    t_pre = graph_us(torch, [prefill] * 4, args.steps, args.warmup)[0]
+    t_dec = graph_us(torch, [decode] * 4, args.steps, args.warmup)[0]
+    t_app = graph_us(torch, [append] * 4, args.steps, args.warmup)[0]
+    per_call, wall = graph_us(torch, [append, prefill, decode], 3 * args.steps, args.warmup)
+    step_us = 3 * per_call  # one step = append + prefill + decode
+    flops = m.prefill_flops()
+    tflops = flops / (t_pre * 1e-6) / 1e12
+    dec_gbps = d.kv_bytes() / (t_dec * 1e-6) / 1e9
+    return {
+        "metric": "mixed chunked-prefill layer-step us (config 5)",
+        "value": round(step_us, 2),
+        "unit": "us/layer-step",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_us / 1e3, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) pool and queries; scattered block tables)",
+        "config": {"workload": m.name, "chunks": "4 x 512 tokens after 0/1k/2k/3k cached",
+                   "decode_batch": d.batch, "num_heads": nh, "head_dim": hd,
+                   "timing": "hipgraph replay"},  # fmt: skip
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(tflops, 1),
+            "peak": MFMA_BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+            "traffic": None,
+        },
+        "prefill_us": round(t_pre, 2),
+        "prefill_gflop": round(flops / 1e9, 2),
+        "decode_us": round(t_dec, 2),
+        "decode_gbps": round(dec_gbps, 1),
+        "append_us": round(t_app, 2),
+        "timed_wall_s": round(wall, 4),
+    }
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only (the decode path has no "
+              "cross-GPU exchange on one box); run with --gpus 1", file=sys.stderr)  # fmt: skip
+        return 2
+
+    import torch
+
+    line = bench_mixed(args, torch) if args.config == "c5" else bench_decode(args, torch)
     if args.copy_calibration:
-        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda:0")
         dst = torch.empty_like(src)
         for _ in range(5):
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(step, args.cpu_seconds)
     print(json.dumps(line), flush=True)
     return 0
 

@@ -198,4 +198,85 @@ def custom(ctx_list, nh, nkv, hd, block_size, dtype, device="cpu", seed: int = 0
                    nkv, hd, dtype, device, gd)  # fmt: skip
 
 
+@dataclass
+class MixedStep:
+    """A chunked-prefill step: prompt chunks and decode sequences over one pool."""
+
+    name: str
+    k_cache: torch.Tensor
+    v_cache: torch.Tensor
+    block_size: int
+    # prompt chunks
+    q_chunks: torch.Tensor  # [T, nh, hd]
+    chunk_tables: torch.Tensor  # [C, W] int32
+    chunk_ctx: torch.Tensor  # [C] int32 (own tokens included)
+    cu_q: torch.Tensor  # [C + 1] int32
+    max_query_len: int
+    # decode rows
+    decode: DecodeStep
+    # this step's new K/V rows (chunk tokens, then decode tokens) and their slots
+    new_k: torch.Tensor
+    new_v: torch.Tensor
+    slot_mapping: torch.Tensor
+    info: dict = field(default_factory=dict)
+
+    def prefill_flops(self) -> int:
+        """Algorithmic FLOPs of the chunk attention: 4 * hd per (query head, visible key)."""
+        nh, hd = self.q_chunks.shape[1], self.q_chunks.shape[2]
+        pairs = 0
+        for c in range(self.chunk_ctx.numel()):
+            ql = int(self.cu_q[c + 1] - self.cu_q[c])
+            prefix = int(self.chunk_ctx[c]) - ql
+            pairs += ql * prefix + ql * (ql + 1) // 2
+        return pairs * nh * hd * 4
+
+
+def config5(device="cpu", seed: int = 0) -> MixedStep:
+    """Mixed chunked-prefill step at the Llama-3-8B shape (32 q heads, 8 KV heads, hd
+    128, bf16, block 16): 4 prompt chunks of 512 tokens, chunk i after a cached prefix
+    of i * 1024 tokens, plus 120 decode sequences with contexts U[256, 2048]."""
+    g = torch.Generator().manual_seed(seed)
+    gd = _gen(device, seed + 1)
+    bs, nh, nkv, hd, dt = 16, 32, 8, 128, torch.bfloat16
+    chunk_len = 512
+    chunk_ctx = [chunk_len + 1024 * i for i in range(4)]
+    dec_ctx = torch.randint(256, 2049, (120,), generator=g).tolist()
+    all_ctx = chunk_ctx + dec_ctx
+    width = max(-(-n // bs) for n in all_ctx)
+    tables, nblk = _scattered(all_ctx, bs, 1.5, width, g)
+    k = _randn((nblk * bs, nkv, hd), dt, device, g=gd)
+    v = _randn((nblk * bs, nkv, hd), dt, device, g=gd)
+
+    def table_tensor(rows):
+        t = torch.zeros(len(rows), width, dtype=torch.int32)
+        for i, r in enumerate(rows):
+            t[i, : len(r)] = torch.tensor(r, dtype=torch.int32)
+        return t.to(device)
+
+    slots = []
+    for t, n in zip(tables[:4], chunk_ctx, strict=True):
+        slots += [t[p // bs] * bs + p % bs for p in range(n - chunk_len, n)]
+    for t, n in zip(tables[4:], dec_ctx, strict=True):
+        slots.append(t[(n - 1) // bs] * bs + (n - 1) % bs)
+    n_new = len(slots)
+    decode = DecodeStep(
+        name="c5_decode", q=_randn((120, nh, hd), dt, device, gd), k_cache=k, v_cache=v,
+        block_tables=table_tensor(tables[4:]),
+        context_lens=torch.tensor(dec_ctx, dtype=torch.int32, device=device), block_size=bs,
+        new_k=torch.empty(0), new_v=torch.empty(0),
+        slot_mapping=torch.tensor(slots[4 * chunk_len :], dtype=torch.int64, device=device),
+    )  # fmt: skip
+    return MixedStep(
+        name="c5_mixed_llama8b_bf16", k_cache=k, v_cache=v, block_size=bs,
+        q_chunks=_randn((4 * chunk_len, nh, hd), dt, device, gd),
+        chunk_tables=table_tensor(tables[:4]),
+        chunk_ctx=torch.tensor(chunk_ctx, dtype=torch.int32, device=device),
+        cu_q=torch.tensor([chunk_len * i for i in range(5)], dtype=torch.int32, device=device),
+        max_query_len=chunk_len, decode=decode,
+        new_k=_randn((n_new, nkv, hd), dt, device, gd),
+        new_v=_randn((n_new, nkv, hd), dt, device, gd),
+        slot_mapping=torch.tensor(slots, dtype=torch.int64, device=device),
+    )  # fmt: skip
+
+
 CONFIGS = {"c1": config1, "c2": config2, "c3": config3, "c4": config4}
