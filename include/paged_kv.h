@@ -125,6 +125,7 @@ int pkv_paged_decode(void* out, int out_dtype, int64_t out_stride_b, int64_t out
  * or fp16; head_dim in {32, 64, 128, 256}. max_query_len bounds every chunk's length
  * (it sizes the grid, so one hipGraph capture serves every length up to it). Block ids
  * must address the pool (out-of-range ids are clamped for memory safety only).
+ * scale must be positive and finite (PKV_E_SHAPE otherwise).
  * Softmax statistics are fp32; for the P.V product the probabilities enter the matrix
  * cores as fp16 (fp16 caches) or as a bf16 hi + lo pair (bf16 caches).
  */

@@ -32,6 +32,15 @@ constexpr int kWave = 64;
 #ifndef PKV_DECODE_PREFETCH
 #define PKV_DECODE_PREFETCH 1
 #endif
+#ifndef PKV_PREFILL_STAGES
+#define PKV_PREFILL_STAGES 2
+#endif
+#ifndef PKV_PREFILL_WAVES_PER_SIMD
+#define PKV_PREFILL_WAVES_PER_SIMD 2
+#endif
+#ifndef PKV_PREFILL_SETPRIO
+#define PKV_PREFILL_SETPRIO 0
+#endif
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
@@ -1062,61 +1071,174 @@ typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 template <int DT> struct Mfma16x16x32Bits;  // MFMA on raw 16-bit bit patterns
 template <> struct Mfma16x16x32Bits<PKV_BF16> {
   typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+  typedef __bf16 v2 __attribute__((ext_vector_type(2)));
+  // bf16 keeps 8 significant bits, too few for softmax weights at a 2e-3 output bar, so
+  // P enters the product as hi = bf16(P) plus lo = bf16(P - hi) (two MFMAs).
+  static constexpr bool kSplit = true;
   __device__ static f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8, a),
                                                    __builtin_bit_cast(v8, b), c, 0, 0, 0);
   }
-  // two fp32 -> one dword of two bf16 (round to nearest even)
-  __device__ static uint32_t pack(float lo, float hi) {
-    return (uint32_t)Elt<PKV_BF16>::from_f32(lo) | ((uint32_t)Elt<PKV_BF16>::from_f32(hi) << 16);
+  // 8 finite fp32 -> hi and lo operand fragments (v_cvt_pk_bf16_f32, round to nearest
+  // even).
+  __device__ static void pack8(const float* p, u32x4& hi, u32x4& lo) {
+    uint32_t h[4], l[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      h[i] = __builtin_bit_cast(uint32_t, v2{(__bf16)p[2 * i], (__bf16)p[2 * i + 1]});
+      // the empty asm keeps h[i] one value (no second conversion to rebuild its low half)
+      uint32_t hv = h[i];
+      __asm__("" : "+v"(hv));
+      const float r0 = p[2 * i] - __uint_as_float(hv << 16);
+      const float r1 = p[2 * i + 1] - __uint_as_float(hv & 0xFFFF0000u);
+      l[i] = __builtin_bit_cast(uint32_t, v2{(__bf16)r0, (__bf16)r1});
+    }
+    hi = u32x4{h[0], h[1], h[2], h[3]};
+    lo = u32x4{l[0], l[1], l[2], l[3]};
   }
 };
 template <> struct Mfma16x16x32Bits<PKV_F16> {
   typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+  typedef _Float16 v2 __attribute__((ext_vector_type(2)));
+  static constexpr bool kSplit = false;  // fp16 keeps 11 bits: P rounded once
   __device__ static f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8, a),
                                                   __builtin_bit_cast(v8, b), c, 0, 0, 0);
   }
-  __device__ static uint32_t pack(float lo, float hi) {
-    return (uint32_t)Elt<PKV_F16>::from_f32(lo) | ((uint32_t)Elt<PKV_F16>::from_f32(hi) << 16);
+  __device__ static void pack8(const float* p, u32x4& hi, u32x4& lo) {
+    uint32_t h[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      h[i] = __builtin_bit_cast(uint32_t, v2{(_Float16)p[2 * i], (_Float16)p[2 * i + 1]});
+    hi = u32x4{h[0], h[1], h[2], h[3]};
+    lo = hi;
   }
 };
 
-template <int DT, int HD>
-__global__ void __launch_bounds__(256)
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding: vmcnt in
+// bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8). Direct-to-LDS loads count in vmcnt and
+// complete in issue order like every other vector-memory load.
+template <int N> __device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit field");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+// Wait for every outstanding LDS access of this wave.
+__device__ __forceinline__ void wait_lgkm0() {
+  __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// LDS byte address of a __shared__ object.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const lds_void*)p;
+}
+
+// Global memory straight into LDS, one wave at a time: lane i's 16 (4) bytes land at LDS
+// address lds_base + 16 i (+ 4 i); lds_base is wave-uniform and travels in M0. Written
+// as inline asm on purpose: the compiler then neither treats the load as a pending LDS
+// write (which makes it wait for every outstanding load before each later LDS read) nor
+// counts it when it sizes its own vmcnt waits. Kernels that use these issue no other
+// vector-memory loads in the same loop and order everything with wait_vmcnt and
+// barriers themselves.
+__device__ __forceinline__ void dma16_to_lds(const void* src, uint32_t lds_base) {
+  asm volatile("global_load_lds_dwordx4 %0, off" : : "v"(src), "{m0}"(lds_base) : "memory");
+}
+__device__ __forceinline__ void dma4_to_lds(const void* src, uint32_t lds_base) {
+  asm volatile("global_load_lds_dword %0, off" : : "v"(src), "{m0}"(lds_base) : "memory");
+}
+
+// Wave priority around runs of MFMAs: when two waves share a SIMD, the one about to
+// issue matrix instructions goes first while the other does its softmax arithmetic.
+__device__ __forceinline__ void mfma_phase_begin() {
+#if PKV_PREFILL_SETPRIO
+  __builtin_amdgcn_s_setprio(1);
+#endif
+}
+__device__ __forceinline__ void mfma_phase_end() {
+#if PKV_PREFILL_SETPRIO
+  __builtin_amdgcn_s_setprio(0);
+#endif
+}
+
+template <int HD> struct PrefillShape {
+  static constexpr int RT = HD >= 256 ? 1 : 2;   // 16-row MFMA tiles per wave
+  static constexpr int BM = 4 * 16 * RT;         // query rows per workgroup (4 waves)
+  static constexpr int KT = HD >= 256 ? 32 : 64; // keys per tile
+  static constexpr int CH = HD / 8;              // 16-byte granules per K/V row
+  static constexpr int NBETA = KT / 16;          // 16-key blocks of S^T per tile
+  static constexpr int NSG = KT / 32;            // 32-key contraction steps of O^T per tile
+  static constexpr int KS = HD / 32;             // contraction steps over head_dim
+  static constexpr int DTL = HD / 16;            // 16-dim tiles of O^T
+  static constexpr int NLD = KT * CH / 256;      // granules per thread per tile, K and V each
+  static constexpr int STAGE = 2 * KT * CH;      // granules per ring stage (K, then V)
+  static constexpr int NSTAGE = PKV_PREFILL_STAGES;  // ring depth: NSTAGE-1 tiles load during one
+  static_assert(NLD >= 1 && KT * CH % 256 == 0, "tile must split evenly over 256 threads");
+  static_assert(2 * NLD < 64, "vmcnt range");
+  static_assert(KT <= kWave, "a tile's block ids must fit one 64-entry table window");
+  // LDS position of chunk c of key t's row is c ^ swz(t). With 16 chunks per row (head
+  // dim 128) swz rotates the token's low 4 bits left by one: the K operand reads (16
+  // consecutive keys, one chunk) and the V^T transpose reads (8 consecutive keys, chunks
+  // 2d and 2d + 1) then both hit distinct banks; a plain t % 16 makes keys x and x ^ 1
+  // collide in the transpose reads.
+  __device__ static int swz(int t) {
+    if constexpr (CH == 16) return ((t << 1) | ((t >> 3) & 1)) & 15;
+    else return t % CH;
+  }
+};
+
+template <int V> using ic = std::integral_constant<int, V>;
+
+template <int DT, int HD, bool POW2>
+__global__ void __launch_bounds__(256, PKV_PREFILL_WAVES_PER_SIMD)
 paged_prefill_kernel(const PrefillArgs a) {
-  constexpr int KT = 64;        // keys per tile
-  constexpr int CH = HD / 8;    // 16-byte chunks per K/V row
-  constexpr int KS = HD / 32;   // MFMA k-steps over head_dim
-  constexpr int DTL = HD / 16;  // 16-dim tiles of O^T
-  constexpr int NLD = KT * CH / 256;  // 16-byte loads per thread per tile, K and V each
+  using SH = PrefillShape<HD>;
+  constexpr int RT = SH::RT, BM = SH::BM, KT = SH::KT, CH = SH::CH, NBETA = SH::NBETA;
+  constexpr int NSG = SH::NSG, KS = SH::KS, DTL = SH::DTL, NLD = SH::NLD;
+  constexpr int STAGE = SH::STAGE, NSTAGE = SH::NSTAGE;
   static_assert(HD % 32 == 0 && HD <= 256, "head_dim must be 32..256, a multiple of 32");
   using MMA = Mfma16x16x32Bits<DT>;
   using S = typename Elt<DT>::S;
-  __shared__ __align__(16) u32x4 k_lds[KT * CH];
-  __shared__ __align__(16) u32x4 v_lds[KT * CH];
+  __shared__ __align__(16) u32x4 ring[NSTAGE * STAGE];      // K/V tiles
+  __shared__ __align__(16) int32_t idring[NSTAGE][4][kWave];  // block-table windows, per wave
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
-  const int wave = tid / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int col = lane & 15, grp = lane >> 4;
-  const int c = blockIdx.z, kvh = blockIdx.y;
+  const int kvh = blockIdx.y;
+
+  // Chunks are taken longest context first (blockIdx.z = rank), and inside a chunk the
+  // last row blocks (which see the most keys) first, so the longest workgroups start
+  // earliest. Each wave ranks up to 64 chunks by itself; larger batches keep their order.
+  int c = blockIdx.z;
+  if (a.n_chunks <= kWave) {
+    const int cap0 = a.max_blocks * a.bs;
+    const int mine = lane < a.n_chunks ? min(max(a.ctx[lane], 0), cap0) : -1;
+    int rank = 0;
+    for (int j = 0; j < a.n_chunks; ++j) {
+      const int other = __shfl(mine, j);
+      rank += (other > mine) || (other == mine && j < lane);
+    }
+    const uint64_t hit = __ballot(lane < a.n_chunks && rank == (int)blockIdx.z);
+    c = __builtin_ctzll(hit);
+  }
   const int q0 = a.cu_q[c], qlen = a.cu_q[c + 1] - q0;
   const int G = a.groups;
   const int nrows = qlen * G;
-  const int rho0 = blockIdx.x * 128;
+  const int rho0 = (a.row_blocks - 1 - (int)blockIdx.x) * BM;
   if (qlen <= 0 || rho0 >= nrows) return;  // uniform per workgroup
   const int cap = a.max_blocks * a.bs;
   const int n = min(max(a.ctx[c], 0), cap);
   const int base_pos = n - qlen;  // position of query token 0
 
-  // This lane's query row in each of its wave's two 16-row tiles (B operand column).
-  int row_tok[2];
-  bool row_ok[2];
-  u32x4 qf[2][KS];
+  // This lane's query row in each of its wave's 16-row tiles (B operand column).
+  int row_tok[RT];
+  bool row_ok[RT];
+  u32x4 qf[RT][KS];
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int rho = rho0 + 32 * wave + 16 * t + col;
+  for (int t = 0; t < RT; ++t) {
+    const int rho = rho0 + 16 * RT * wave + 16 * t + col;
     row_ok[t] = rho < nrows;
     const int rr = row_ok[t] ? rho : 0;
     row_tok[t] = rr / G;
@@ -1126,170 +1248,268 @@ paged_prefill_kernel(const PrefillArgs a) {
     for (int s = 0; s < KS; ++s) qf[t][s] = *reinterpret_cast<const u32x4*>(qp + 32 * s);
   }
   // Keys any row of this workgroup attends to: [0, kend).
-  const int last_row = min(nrows - 1, rho0 + 127);
+  const int last_row = min(nrows - 1, rho0 + BM - 1);
   const int kend = min(n, base_pos + last_row / G + 1);
   const int ntiles = kend > 0 ? (kend + KT - 1) / KT : 0;
 
-  // Next tile's K/V in registers: thread tid fills LDS granules r * 256 + tid; granule
-  // (token t, position p) holds chunk p ^ (t % CH) of that token's row. Tokens past the
-  // context re-read the last context token (finite data, masked out of the softmax).
-  const int64_t tbl_row = (int64_t)c * a.table_stride;
-  u32x4 kst[NLD], vst[NLD];
-  auto fetch = [&](int kt0) {
+  // Tile j's K/V rows go from the pool straight into ring stage j % NSTAGE. Instruction
+  // r of wave w fills granules r*256 + 64w .. +63 of a stage, one per lane; granule
+  // (token t, position p) holds chunk p ^ (t % CH) of that token's row, so the MFMA
+  // operand reads below are conflict-free. Positions past the context re-read the last
+  // context token (finite, masked out of the softmax). The 64 block-table entries from
+  // the tile's first block on reach LDS the same way, one tile ahead of the K/V loads
+  // that need them, so the table lookup is never on a tile's critical path.
+  int tok[NLD], chk[NLD];
 #pragma unroll
-    for (int r = 0; r < NLD; ++r) {
-      const int gi = r * 256 + tid;
-      const int t = gi / CH;
-      const int chunk = (gi % CH) ^ (t % CH);
-      const int p = min(kt0 + t, n - 1);
-      const int blk = a.bs_shift >= 0 ? (p >> a.bs_shift) : p / a.bs;
-      const int bid = a.tables[tbl_row + blk];
-      int64_t sl = (int64_t)bid * a.bs + (p - blk * a.bs);
-      sl = (sl >= 0 && sl < a.num_slots) ? sl : 0;
-      const int64_t off = sl * a.kv_ss + (int64_t)kvh * a.kv_sh + chunk * 8;
-      kst[r] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const S*>(a.k) + off);
-      vst[r] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const S*>(a.v) + off);
-    }
+  for (int r = 0; r < NLD; ++r) {
+    const int gi = r * 256 + tid;
+    tok[r] = gi / CH;
+    chk[r] = (gi % CH) ^ SH::swz(tok[r]);
+  }
+  const int32_t* trow = a.tables + (int64_t)c * a.table_stride;
+  const int nlast = max(n - 1, 0);
+  auto blk_of = [&](int p) { return POW2 ? (p >> a.bs_shift) : p / a.bs; };
+  const int blast = blk_of(nlast);
+  const uint32_t ring_lds = lds_addr(ring);
+  const uint32_t ids_lds = lds_addr(&idring[0][wave][0]);
+  auto issue_ids = [&](int it) {
+    const int st = it % NSTAGE;
+    const int b = min(blk_of(it * KT) + lane, blast);
+    dma4_to_lds(trow + b, ids_lds + (uint32_t)(st * 4 * kWave * 4));
   };
-  auto stash = [&]() {
+  // One DMA instruction of one wave covers SEG consecutive keys of a tile. When the block
+  // size is a power of two >= SEG those keys share one block: its id is wave-uniform and
+  // the address is scalar math plus one per-lane offset.
+  constexpr int SEG = kWave / CH;
+  const bool seg_uniform = POW2 && a.bs >= SEG;
+  auto issue_kv = [&](int it) {
+    const int st = it % NSTAGE;
+    const int32_t* ids = &idring[st][wave][0];
+    const int b0 = blk_of(it * KT);
+    const uint32_t stage = ring_lds + (uint32_t)(st * STAGE * 16);
+    if constexpr (POW2) {
+      if (seg_uniform) {
+#pragma unroll
+        for (int r = 0; r < NLD; ++r) {
+          const int seg = it * KT + (r * 256 + wave * kWave) / CH;  // first key, uniform
+          const int blk = min(seg >> a.bs_shift, blast);
+          int64_t id = __builtin_amdgcn_readfirstlane(ids[blk - b0]);
+          if (id < 0 || (id + 1) * a.bs > a.num_slots) id = 0;  // memory safety only
+          const int64_t base = (id * a.bs * a.kv_ss + (int64_t)kvh * a.kv_sh) * (int64_t)sizeof(S);
+          const int in_blk = min(seg + lane / CH, nlast) - blk * a.bs;
+          const uint32_t lo = (uint32_t)((in_blk * a.kv_ss + chk[r] * 8) * (int64_t)sizeof(S));
+          const uint32_t dk = stage + (uint32_t)((r * 256 + wave * kWave) * 16);
+          dma16_to_lds(reinterpret_cast<const char*>(a.k) + base + lo, dk);
+          dma16_to_lds(reinterpret_cast<const char*>(a.v) + base + lo,
+                       dk + (uint32_t)(KT * CH * 16));
+        }
+        return;
+      }
+    }
 #pragma unroll
     for (int r = 0; r < NLD; ++r) {
-      k_lds[r * 256 + tid] = kst[r];
-      v_lds[r * 256 + tid] = vst[r];
+      const int p = min(it * KT + tok[r], nlast);
+      const int blk = blk_of(p);
+      int64_t sl = (int64_t)ids[blk - b0] * a.bs + (p - blk * a.bs);
+      sl = (sl >= 0 && sl < a.num_slots) ? sl : 0;
+      const int64_t off = sl * a.kv_ss + (int64_t)kvh * a.kv_sh + chk[r] * 8;
+      const uint32_t dk = stage + (uint32_t)((r * 256 + wave * kWave) * 16);
+      dma16_to_lds(reinterpret_cast<const S*>(a.k) + off, dk);
+      dma16_to_lds(reinterpret_cast<const S*>(a.v) + off, dk + (uint32_t)(KT * CH * 16));
     }
   };
 
-  float m_run[2], l_run[2];
-  f32x4 o[2][DTL];
+  float m_run[RT], l_run[RT];
+  f32x4 o[RT][DTL];
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
+  for (int t = 0; t < RT; ++t) {
     m_run[t] = -INFINITY;
     l_run[t] = 0.f;
 #pragma unroll
     for (int d = 0; d < DTL; ++d) o[t][d] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  if (ntiles > 0) {
-    fetch(0);
-    stash();
-    __syncthreads();
-  }
-  for (int it = 0; it < ntiles; ++it) {
-    const int kt0 = it * KT;
-    if (it + 1 < ntiles) fetch(kt0 + KT);  // in flight while this tile is reduced
+  // Rows whose causal limit a tile can cross: tile j needs the mask only if it reaches
+  // past the smallest limit among this workgroup's rows (its first row's).
+  const int limit_min = min(n - 1, base_pos + rho0 / G);
+  int limit[RT];  // last key each of this lane's rows sees
+#pragma unroll
+  for (int t = 0; t < RT; ++t) limit[t] = min(n - 1, base_pos + row_tok[t]);
+
+  // Per-lane LDS byte offsets of the operand fragments inside a stage.
+  //   K: lane (col, grp) reads key 16 beta + col, chunk 4 s + grp. swz(key) depends on
+  //      beta only when a row has more than 16 chunks (head_dim 256).
+  //   V^T: lane (col, grp) reads key 32 sg + 16 h2 + 4 grp + col / 4, dims 16 d +
+  //      4 (col % 4) .. +4 (chunk 2 d + (col % 4) / 2, half (col % 4) & 1).
+  constexpr int KSW = CH > 16 ? NBETA : 1;
+  constexpr int VSW = CH > 16 ? 2 : 1;
+  uint32_t koff[KSW][KS], voff[VSW][DTL];
+#pragma unroll
+  for (int b = 0; b < KSW; ++b)
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const int tk = 16 * b + col;
+      koff[b][s] = (uint32_t)(((4 * s + grp) ^ SH::swz(tk)) * 16 + col * CH * 16);
+    }
+#pragma unroll
+  for (int h2 = 0; h2 < VSW; ++h2)
+#pragma unroll
+    for (int d = 0; d < DTL; ++d) {
+      const int tk = 16 * h2 + 4 * grp + col / 4;
+      const int chunk = 2 * d + (col % 4) / 2;
+      voff[h2][d] = (uint32_t)(((chunk ^ SH::swz(tk)) * 16 + (col % 4 & 1) * 8) +
+                               (4 * grp + col / 4) * CH * 16);
+    }
+
+  // One tile of work on ring stage j % NSTAGE; MASK: some key of the tile is past some row's
+  // causal limit (only the tiles on the diagonal and at the context end).
+  auto compute = [&](int j, auto MASK) {
+    constexpr bool masked = decltype(MASK)::value != 0;
+    const int kt0 = j * KT;
+    const char* stage = reinterpret_cast<const char*>(ring) + (j % NSTAGE) * STAGE * 16;
+    // Operand fragments come from LDS at a per-lane offset (koff / voff) plus a
+    // compile-time constant: K by 16-byte reads, V^T by ds_read_b64_tr_b16 transpose
+    // reads.
+    auto kfrag = [&](int beta, int s) {
+      return *reinterpret_cast<const u32x4*>(stage + beta * 16 * CH * 16 +
+                                             koff[KSW == 1 ? 0 : beta][s]);
+    };
+    const char* vstage = stage + KT * CH * 16;
+    auto vfrag = [&](int sg, int d) {
+      u32x4 v;
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        // generic -> LDS address space (an addrspacecast of a __shared__ pointer)
+        const s16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_s16x4*)(vstage + (32 * sg + 16 * h2) * CH * 16 + voff[VSW == 1 ? 0 : h2][d]));
+        const uint32_t lo = (uint32_t)(uint16_t)x[0] | ((uint32_t)(uint16_t)x[1] << 16);
+        const uint32_t hi = (uint32_t)(uint16_t)x[2] | ((uint32_t)(uint16_t)x[3] << 16);
+        if (h2 == 0) { v.x = lo; v.y = hi; } else { v.z = lo; v.w = hi; }
+      }
+      return v;
+    };
 
     // S^T = K . Q^T: block beta holds keys 16 beta + 4 grp + r for query row col.
-    f32x4 sc[4][2];
+    f32x4 sc[RT][NBETA];
+    mfma_phase_begin();
 #pragma unroll
-    for (int beta = 0; beta < 4; ++beta) {
-      sc[beta][0] = sc[beta][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-      const int t = 16 * beta + col;
+    for (int beta = 0; beta < NBETA; ++beta) {
+#pragma unroll
+      for (int t = 0; t < RT; ++t) sc[t][beta] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        const u32x4 ka = k_lds[t * CH + ((4 * s + grp) ^ (t % CH))];
-        sc[beta][0] = MMA::mma(ka, qf[0][s], sc[beta][0]);
-        sc[beta][1] = MMA::mma(ka, qf[1][s], sc[beta][1]);
+        const u32x4 kf = kfrag(beta, s);
+#pragma unroll
+        for (int t = 0; t < RT; ++t) sc[t][beta] = MMA::mma(kf, qf[t][s], sc[t][beta]);
       }
     }
+    mfma_phase_end();
 
-    // Online softmax per query row; P^T fragments for the second product. bf16 keeps
-    // 8 significant bits, too few for P at the 2e-3 bar, so for bf16 P is also split
-    // into hi = bf16(P) and lo = bf16(P - hi) and both are multiplied into O.
-    constexpr bool kSplitP = DT == PKV_BF16;
-    u32x4 pb[2][2];  // [row tile][key half sigma]
-    u32x4 pl[2][2];  // low parts (kSplitP)
+
+    u32x4 pb[RT][NSG], pl[RT][NSG];  // P^T fragments (hi, lo)
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int limit = min(n - 1, base_pos + row_tok[t]);  // last key this row sees
-      float p[4][4];
+    for (int t = 0; t < RT; ++t) {
+      // Online softmax of row col in the log2 domain, p = exp2(scale_log2 * s - m_run).
+      // The reference m_run is raised only when a score exceeds it by more than 2^8:
+      // a stale reference changes nothing in O / l (both carry the same factor), keeps
+      // p <= 256, and leaves O untouched on most tiles.
+      if constexpr (masked) {
+#pragma unroll
+        for (int beta = 0; beta < NBETA; ++beta)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (kt0 + 16 * beta + 4 * grp + r > limit[t]) sc[t][beta][r] = -INFINITY;
+      }
       float mx = -INFINITY;
 #pragma unroll
-      for (int beta = 0; beta < 4; ++beta)
+      for (int beta = 0; beta < NBETA; ++beta)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int kpos = kt0 + 16 * beta + 4 * grp + r;
-          p[beta][r] = (row_ok[t] && kpos <= limit) ? sc[beta][t][r] * a.scale_log2 : -INFINITY;
-          mx = fmaxf(mx, p[beta][r]);
-        }
-      mx = rows_max(mx);
-      const float mn = fmaxf(m_run[t], mx);
-      const float mref = mn == -INFINITY ? 0.f : mn;
-      const float alpha = __builtin_amdgcn_exp2f(m_run[t] - mref);
-      m_run[t] = mn;
+        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sc[t][beta][r]);
+      mx = rows_max(mx) * a.scale_log2;
+      const bool raise = mx > m_run[t] + 8.f;  // also true the first time (m_run = -inf)
+      if (__builtin_amdgcn_ballot_w64(raise)) {  // wave-uniform
+        const float mn = raise ? mx : m_run[t];
+        const float alpha = __builtin_amdgcn_exp2f(m_run[t] - mn);  // 0 when m_run = -inf
+        m_run[t] = mn;
+        l_run[t] *= alpha;
+#pragma unroll
+        for (int d = 0; d < DTL; ++d) o[t][d] *= alpha;
+      }
+      const float mref = m_run[t] == -INFINITY ? 0.f : m_run[t];
       float psum = 0.f;
 #pragma unroll
-      for (int beta = 0; beta < 4; ++beta)
+      for (int sg = 0; sg < NSG; ++sg) {
+        float p[8];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          p[beta][r] = __builtin_amdgcn_exp2f(p[beta][r] - mref);
-          psum += p[beta][r];
+        for (int e = 0; e < 8; ++e) {
+          p[e] = __builtin_amdgcn_exp2f(
+              __builtin_fmaf(sc[t][2 * sg + e / 4][e % 4], a.scale_log2, -mref));
+          psum += p[e];
         }
-      l_run[t] = __builtin_fmaf(l_run[t], alpha, psum);
-#pragma unroll
-      for (int d = 0; d < DTL; ++d) o[t][d] *= alpha;
-#pragma unroll
-      for (int sg = 0; sg < 2; ++sg) {
-        const float* a0 = p[2 * sg];
-        const float* a1 = p[2 * sg + 1];
-        pb[t][sg] = u32x4{MMA::pack(a0[0], a0[1]), MMA::pack(a0[2], a0[3]),
-                          MMA::pack(a1[0], a1[1]), MMA::pack(a1[2], a1[3])};
-        if constexpr (kSplitP) {
-          float r[8];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            r[e] = a0[e] - Elt<DT>::to_f32(Elt<DT>::from_f32(a0[e]));
-            r[4 + e] = a1[e] - Elt<DT>::to_f32(Elt<DT>::from_f32(a1[e]));
-          }
-          pl[t][sg] = u32x4{MMA::pack(r[0], r[1]), MMA::pack(r[2], r[3]),
-                            MMA::pack(r[4], r[5]), MMA::pack(r[6], r[7])};
-        }
+        // P^T fragment: the lane's own 8 probabilities (keys 32 sg + 16 (e / 4) + 4 grp
+        // + e % 4), matching the transpose-read order of V^T.
+        MMA::pack8(p, pb[t][sg], pl[t][sg]);
       }
+      l_run[t] += psum;
     }
 
-    // O^T += V^T . P^T. Lane col of group grp supplies token 32 sg + 4 grp + col / 4
-    // (+16 for the second read), dims 16 d + 4 (col % 4): the transpose read hands
-    // each lane 4 consecutive keys of one head dim.
-    char* vbytes = reinterpret_cast<char*>(v_lds);
+    // O^T += V^T . P^T; each V^T fragment serves every row tile.
+    mfma_phase_begin();
 #pragma unroll
-    for (int sg = 0; sg < 2; ++sg) {
+    for (int sg = 0; sg < NSG; ++sg)
 #pragma unroll
       for (int d = 0; d < DTL; ++d) {
-        u32x4 va;
+        const u32x4 vf = vfrag(sg, d);
 #pragma unroll
-        for (int h2 = 0; h2 < 2; ++h2) {
-          const int t = 32 * sg + 16 * h2 + 4 * grp + col / 4;
-          const int dim = 16 * d + 4 * (col % 4);
-          const int gran = t * CH + ((dim / 8) ^ (t % CH));
-          const int byte = gran * 16 + ((dim / 4) & 1) * 8;
-          // generic -> LDS address space (an addrspacecast of a __shared__ pointer)
-          const s16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vbytes + byte));
-          const uint32_t lo = (uint32_t)(uint16_t)x[0] | ((uint32_t)(uint16_t)x[1] << 16);
-          const uint32_t hi = (uint32_t)(uint16_t)x[2] | ((uint32_t)(uint16_t)x[3] << 16);
-          if (h2 == 0) { va.x = lo; va.y = hi; } else { va.z = lo; va.w = hi; }
-        }
-        o[0][d] = MMA::mma(va, pb[0][sg], o[0][d]);
-        o[1][d] = MMA::mma(va, pb[1][sg], o[1][d]);
-        if constexpr (kSplitP) {
-          o[0][d] = MMA::mma(va, pl[0][sg], o[0][d]);
-          o[1][d] = MMA::mma(va, pl[1][sg], o[1][d]);
+        for (int t = 0; t < RT; ++t) {
+          o[t][d] = MMA::mma(vf, pb[t][sg], o[t][d]);
+          if constexpr (MMA::kSplit) o[t][d] = MMA::mma(vf, pl[t][sg], o[t][d]);
         }
       }
-    }
+    mfma_phase_end();
+  };
 
-    if (it + 1 < ntiles) {
-      __syncthreads();  // every wave is done with this tile
-      stash();
-      __syncthreads();
-    }
+  // Pipeline, prefetch distance D = NSTAGE - 1. Issue order (per wave):
+  //   ids(0) .. ids(D), [wait all], KV(0) .. KV(D-1), then per tile j:
+  //   wait until KV(j) and ids(j+D) have landed; barrier (every wave's share of KV(j)
+  //   landed, and every wave is done with the stages ids(j+D+1) and KV(j+D) reuse);
+  //   ids(j+D+1); KV(j+D); compute(j).
+  // At the wait the only loads issued after ids(j+D) are the K/V tiles j+1 .. j+D-1 that
+  // exist (2 NLD loads each): waiting down to that many outstanding completes KV(j) and
+  // ids(j+D) (loads complete in issue order). Block ids are always fetched (clamped to
+  // the context's last block), so the counts do not change near the end.
+  constexpr int D = NSTAGE - 1;
+  static_assert(D == 1 || D == 2, "ring of 2 or 3 stages");
+  if (ntiles > 0) {
+#pragma unroll
+    for (int k = 0; k <= D; ++k) issue_ids(k);
+    wait_vmcnt<0>();
+#pragma unroll
+    for (int k = 0; k < D; ++k)
+      if (k < ntiles) issue_kv(k);
+    auto step = [&](int j, auto MASK) {
+      if (D == 2 && j + 1 < ntiles) wait_vmcnt<2 * NLD>();
+      else wait_vmcnt<0>();
+      wait_lgkm0();
+      __builtin_amdgcn_s_barrier();
+      issue_ids(j + D + 1);
+      if (j + D < ntiles) issue_kv(j + D);
+      compute(j, MASK);
+    };
+    // Tile j needs the causal mask iff j * KT + KT - 1 > limit_min: the tiles from
+    // j_mask on. Two loops, so each holds one variant of the tile code.
+    const int j_mask = min(ntiles, max(0, (limit_min + 1) / KT));
+    for (int j = 0; j < j_mask; ++j) step(j, ic<0>{});
+    for (int j = j_mask; j < ntiles; ++j) step(j, ic<1>{});
   }
 
   // O^T lane (row col, grp) holds dims 16 d + 4 grp + r of query row col.
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
+  for (int t = 0; t < RT; ++t) {
     const float l_tot = rows_sum(l_run[t]);
     if (!row_ok[t]) continue;
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    const int rho = rho0 + 32 * wave + 16 * t + col;
+    const int rho = rho0 + 16 * RT * wave + 16 * t + col;
     const int64_t e0 = (int64_t)(q0 + rho / G) * a.out_st + (int64_t)(kvh * G + rho % G) * a.out_sh;
 #pragma unroll
     for (int d = 0; d < DTL; ++d) {
@@ -1480,16 +1700,26 @@ int check_decode_shape(int kv_dtype, int head_dim, int num_heads, int num_kv_hea
 }
 
 
-template <int DT>
-hipError_t launch_prefill(const PrefillArgs& a, int hd, hipStream_t st) {
+template <int DT, int HD>
+hipError_t launch_prefill_hd(PrefillArgs a, int64_t rows, hipStream_t st) {
+  constexpr int BM = PrefillShape<HD>::BM;
+  a.row_blocks = (int)((rows + BM - 1) / BM);
   const dim3 grid((unsigned)a.row_blocks, (unsigned)a.nkv, (unsigned)a.n_chunks), block(256);
-  switch (hd) {
-    case 32: hipLaunchKernelGGL((paged_prefill_kernel<DT, 32>), grid, block, 0, st, a); break;
-    case 64: hipLaunchKernelGGL((paged_prefill_kernel<DT, 64>), grid, block, 0, st, a); break;
-    case 128: hipLaunchKernelGGL((paged_prefill_kernel<DT, 128>), grid, block, 0, st, a); break;
-    default: hipLaunchKernelGGL((paged_prefill_kernel<DT, 256>), grid, block, 0, st, a);
-  }
+  if (a.bs_shift >= 0)
+    hipLaunchKernelGGL((paged_prefill_kernel<DT, HD, true>), grid, block, 0, st, a);
+  else
+    hipLaunchKernelGGL((paged_prefill_kernel<DT, HD, false>), grid, block, 0, st, a);
   return hipGetLastError();
+}
+
+template <int DT>
+hipError_t launch_prefill(const PrefillArgs& a, int hd, int64_t rows, hipStream_t st) {
+  switch (hd) {
+    case 32: return launch_prefill_hd<DT, 32>(a, rows, st);
+    case 64: return launch_prefill_hd<DT, 64>(a, rows, st);
+    case 128: return launch_prefill_hd<DT, 128>(a, rows, st);
+    default: return launch_prefill_hd<DT, 256>(a, rows, st);
+  }
 }
 
 }  // namespace
@@ -1695,6 +1925,7 @@ int pkv_paged_prefill(void* out, int out_dtype, int64_t out_stride_tok, int64_t 
     return PKV_E_SHAPE;
   if (!(head_dim == 32 || head_dim == 64 || head_dim == 128 || head_dim == 256)) return PKV_E_SHAPE;
   if ((int64_t)max_blocks * block_size > (int64_t)1 << 30) return PKV_E_SHAPE;
+  if (!(scale > 0.f && scale < INFINITY)) return PKV_E_SHAPE;  // softmax scale
   const int64_t rows = (int64_t)max_query_len * (num_heads / num_kv_heads);
   if (rows > (int64_t)1 << 30) return PKV_E_SHAPE;
   if (n_chunks == 0 || max_query_len == 0) return 0;
@@ -1728,12 +1959,12 @@ int pkv_paged_prefill(void* out, int out_dtype, int64_t out_stride_tok, int64_t 
   a.groups = num_heads / num_kv_heads;
   a.bs = block_size;
   a.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz(block_size) : -1;
-  a.row_blocks = (int)((rows + 127) / 128);
+  a.row_blocks = 0;  // set per head_dim by launch_prefill
   a.scale_log2 = scale * 1.4426950408889634f;
   a.out_f32 = out_dtype == PKV_F32;
   hipStream_t st = (hipStream_t)stream;
-  return (int)(kv_dtype == PKV_BF16 ? launch_prefill<PKV_BF16>(a, head_dim, st)
-                                    : launch_prefill<PKV_F16>(a, head_dim, st));
+  return (int)(kv_dtype == PKV_BF16 ? launch_prefill<PKV_BF16>(a, head_dim, rows, st)
+                                    : launch_prefill<PKV_F16>(a, head_dim, rows, st));
 }
 
 }  // extern "C"
