@@ -71,6 +71,20 @@ int pkv_copy_blocks(void* k_pool, void* v_pool, int64_t layer_stride_bytes,
                     const int64_t* block_mapping, int64_t n_pairs, void* stream);
 
 /*
+ * Slot mapping of a decode step, built on the device: for each sequence b,
+ *   slots[b] = block_tables[b, (n-1) / block_size] * block_size + (n-1) % block_size,
+ * n = context_lens[b] (the new token included), or -1 -- which pkv_kv_append skips --
+ * when n < 1, (n-1) / block_size >= max_blocks, or the slot is outside [0, num_slots).
+ * Replaces the host-side slot lists of PagedBatch._decode and DecodeGraphs.run
+ * (reference engine/runtime/paged_cache.py:140-143, engine/runtime/cuda_graphs.py:104,
+ * engine/runtime/engine.py:208-210), so a captured decode step needs only the tables and
+ * lengths copied in. slots: device int64 [batch].
+ */
+int pkv_decode_slots(int64_t* slots, const int32_t* block_tables, int64_t table_stride,
+                     int32_t max_blocks, const int32_t* context_lens, int32_t batch,
+                     int32_t block_size, int64_t num_slots, void* stream);
+
+/*
  * Workgroups the decode kernel should use on the current device for this shape: as
  * many as the GPU holds resident at once (CUs x workgroups per CU). Depends only on the
  * device and static shapes, so a graph captured with it stays valid. Returns >= 1, or a

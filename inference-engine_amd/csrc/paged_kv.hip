@@ -279,6 +279,31 @@ copy_blocks_kernel(char* __restrict__ k_pool, char* __restrict__ v_pool,
 }
 
 // ---------------------------------------------------------------------------------
+// Decode slot mapping on the device: the slot of each sequence's newest token,
+// table[(n-1) / bs] * bs + (n-1) % bs with n = context_lens[b] (the token appended this
+// step is counted). -1 (skipped by the append) when n < 1, when its block lies past
+// max_blocks, or when the slot falls outside the pool.
+// ---------------------------------------------------------------------------------
+
+__global__ void __launch_bounds__(256)
+decode_slots_kernel(int64_t* __restrict__ slots, const int32_t* __restrict__ tables,
+                    int64_t table_stride, int32_t max_blocks, const int32_t* __restrict__ ctx,
+                    int32_t batch, int32_t bs, int64_t num_slots) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= batch) return;
+  const int n = ctx[b];
+  int64_t slot = -1;
+  if (n >= 1) {
+    const int blk = (n - 1) / bs;
+    if (blk < max_blocks) {
+      const int64_t s = (int64_t)tables[(int64_t)b * table_stride + blk] * bs + (n - 1) % bs;
+      if (s >= 0 && s < num_slots) slot = s;
+    }
+  }
+  slots[b] = slot;
+}
+
+// ---------------------------------------------------------------------------------
 // Paged decode attention: stream-K pass.
 //
 // The contexts of all sequences are cut into units of TILE tokens (a sequence with an
@@ -1811,6 +1836,18 @@ int pkv_copy_blocks(void* k_pool, void* v_pool, int64_t layer_stride_bytes,
                        (char*)v_pool, layer_stride_bytes, block_bytes, num_blocks,
                        block_mapping);
   }
+  return (int)hipGetLastError();
+}
+
+int pkv_decode_slots(int64_t* slots, const int32_t* block_tables, int64_t table_stride,
+                     int32_t max_blocks, const int32_t* context_lens, int32_t batch,
+                     int32_t block_size, int64_t num_slots, void* stream) {
+  if (batch < 0 || max_blocks < 0 || block_size <= 0 || num_slots < 0) return PKV_E_SHAPE;
+  if (batch == 0) return 0;
+  if (!slots || !context_lens || (max_blocks > 0 && !block_tables)) return PKV_E_NULL;
+  hipLaunchKernelGGL(decode_slots_kernel, dim3((unsigned)((batch + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, slots, block_tables, table_stride, max_blocks,
+                     context_lens, batch, block_size, num_slots);
   return (int)hipGetLastError();
 }
 

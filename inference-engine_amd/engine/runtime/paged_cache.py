@@ -9,6 +9,7 @@ decode kernel streams and what ``copy_blocks`` moves.
 
 from __future__ import annotations
 
+from collections.abc import Sequence
 from dataclasses import dataclass
 
 import torch
@@ -142,3 +143,171 @@ def copy_blocks(
         _native.stream_of(dev),
     )  # fmt: skip
     _native.check(status, what)
+
+
+def decode_slots(block_tables: torch.Tensor, context_lens: torch.Tensor, block_size: int,
+                 num_slots: int, out: torch.Tensor | None = None) -> torch.Tensor:  # fmt: skip
+    """Slot of each sequence's newest token, ``table[(n-1)//bs]*bs + (n-1)%bs`` with
+    n = context_lens[b], computed on the device (int64 [B]; -1 where n < 1 or the block
+    lies past the table or the pool: the append skips it). The reference builds these on
+    the host (engine/runtime/paged_cache.py:140-143, engine/runtime/cuda_graphs.py:104);
+    on the device a captured decode step needs only tables and lengths copied in."""
+    what = "decode_slots"
+    dev = _native.require_gpu(what, block_tables, context_lens)
+    if block_tables.dtype != torch.int32 or context_lens.dtype != torch.int32:
+        raise TypeError(f"{what}: block_tables and context_lens must be int32")
+    b = context_lens.numel()
+    if block_tables.dim() != 2 or block_tables.shape[0] != b or block_tables.stride(1) != 1 \
+            or not context_lens.is_contiguous():  # fmt: skip
+        raise ValueError(f"{what}: block_tables [B, W] (unit column stride), context_lens [B]")
+    if out is None:
+        out = torch.empty(b, dtype=torch.int64, device=dev)
+    elif out.dtype != torch.int64 or out.shape != (b,) or not out.is_contiguous():
+        raise ValueError(f"{what}: out must be a contiguous int64 [B] tensor")
+    status = _native.lib().pkv_decode_slots(
+        out.data_ptr(), block_tables.data_ptr(), block_tables.stride(0), block_tables.shape[1],
+        context_lens.data_ptr(), b, block_size, num_slots, _native.stream_of(dev))  # fmt: skip
+    _native.check(status, what)
+    return out
+
+
+@dataclass
+class PagedBatch:
+    """Everything attention needs for one step, built once and shared by all layers
+    (reference engine/runtime/paged_cache.py:52-229, same role and field names where the
+    meaning is the same). A step's new tokens from every sequence are flattened into one
+    row of N tokens; sequence i owns the next query_lens[i] of them.
+
+    Decode steps (every sequence adds one token) read K/V through ``block_tables`` /
+    ``context_lens`` in the decode kernel. Mixed steps send sequences adding one token
+    (``decode_rows``) to the decode kernel and every longer run of new tokens -- a
+    prompt or a prompt chunk, its queries last in its context -- to the chunked-prefill
+    kernel through ``chunk_*``. Nothing is gathered.
+    """
+
+    cache: PagedKVCache
+    slot_mapping: torch.Tensor  # [N] int64: where each new token's K/V is written
+    last_index: torch.Tensor  # [B] flat index of each sequence's last new token
+    use_kernel: bool = True
+    block_tables: torch.Tensor | None = None  # [Bd, W] int32, decode rows
+    context_lens: torch.Tensor | None = None  # [Bd] int32, new token included
+    mixed: bool = False
+    decode_rows: torch.Tensor | None = None  # [Bd] int64 flat token index
+    chunk_rows: torch.Tensor | None = None  # [Tq] int64 flat index of every chunk token
+    chunk_tables: torch.Tensor | None = None  # [C, W] int32
+    chunk_ctx: torch.Tensor | None = None  # [C] int32 context incl. the chunk's tokens
+    cu_seqlens_q: torch.Tensor | None = None  # [C + 1] int32 offsets into chunk_rows
+    max_query_len: int = 0
+    # Per chunk token, for shapes the chunk kernel does not take (fp32, head_dim 16): the
+    # chunk's table row and the context that token sees (causal), for the decode kernel.
+    row_tables: torch.Tensor | None = None  # [Tq, W] int32
+    row_ctx: torch.Tensor | None = None  # [Tq] int32
+    copy_pairs: torch.Tensor | None = None  # [n, 2] int64 (src, dst) copy-on-write
+
+    @classmethod
+    def build(
+        cls,
+        cache: PagedKVCache,
+        block_tables: Sequence[Sequence[int]],
+        context_lens: Sequence[int],
+        query_lens: Sequence[int],
+        device: str | torch.device,
+        use_kernel: bool = True,
+        force_mixed: bool = False,
+        copy_pairs: Sequence[tuple[int, int]] = (),
+        device_slots: bool = False,
+    ) -> PagedBatch:
+        """Per sequence, in flattened order: its block table, its context length after
+        this step (new tokens included) and its number of new tokens (reference :80-127).
+        ``copy_pairs``: copy-on-write (src, dst) block pairs from the block manager, to
+        apply before this step's writes. ``device_slots``: decode steps compute the slot
+        mapping on the device from the uploaded tables instead of on the host."""
+        if not use_kernel:
+            raise ValueError("PagedBatch: this build has only the kernel path (HIP)")
+        if not query_lens:
+            raise ValueError("PagedBatch: empty step")
+        pairs = None
+        if copy_pairs:
+            pairs = torch.tensor(list(copy_pairs), dtype=torch.int64).view(-1, 2).to(device)
+        if max(query_lens) == 1 and not force_mixed:
+            batch = cls._decode(cache, block_tables, context_lens, device, device_slots)
+        else:
+            batch = cls._mixed(cache, block_tables, context_lens, query_lens, device)
+        batch.copy_pairs = pairs
+        return batch
+
+    @staticmethod
+    def _tables(rows: Sequence[Sequence[int]]) -> torch.Tensor:
+        width = max(1, max(len(t) for t in rows))
+        return torch.tensor([list(t) + [0] * (width - len(t)) for t in rows], dtype=torch.int32)
+
+    @classmethod
+    def _decode(cls, cache: PagedKVCache, block_tables, context_lens, device,
+                device_slots: bool) -> PagedBatch:  # fmt: skip
+        """Reference :130-156: tables padded with block 0, the new token's slot."""
+        bs, b = cache.block_size, len(context_lens)
+        tables = cls._tables(block_tables).to(device)
+        ctx = torch.tensor(list(context_lens), dtype=torch.int32, device=device)
+        if device_slots:
+            slots = decode_slots(tables, ctx, bs, cache.k.shape[1])
+        else:
+            slots = torch.tensor(
+                [t[(n - 1) // bs] * bs + (n - 1) % bs
+                 for t, n in zip(block_tables, context_lens, strict=True)],
+                dtype=torch.int64, device=device)  # fmt: skip
+        flat = torch.arange(b, device=device)
+        return cls(cache=cache, slot_mapping=slots, last_index=flat, block_tables=tables,
+                   context_lens=ctx)  # fmt: skip
+
+    @classmethod
+    def _mixed(cls, cache: PagedKVCache, block_tables, context_lens, query_lens,
+               device) -> PagedBatch:  # fmt: skip
+        """Reference :159-229 without the gather: decode rows keep their tables; every
+        run of q > 1 new tokens becomes a chunk whose queries sit at positions
+        ctx - q .. ctx - 1 of its context (bottom-right causal)."""
+        bs = cache.block_size
+        slots: list[int] = []
+        dec_rows, dec_tables, dec_ctx = [], [], []
+        ch_rows, ch_tables, ch_ctx, ch_q = [], [], [], []
+        start = 0
+        for table, ctx, q in zip(block_tables, context_lens, query_lens, strict=True):
+            if q < 1 or ctx < q:
+                raise ValueError(f"PagedBatch: {q} new tokens in a context of {ctx}")
+            if -(-ctx // bs) > len(table):
+                raise ValueError(f"PagedBatch: a table of {len(table)} blocks cannot hold "
+                                 f"{ctx} tokens")  # fmt: skip
+            slots.extend(table[p // bs] * bs + p % bs for p in range(ctx - q, ctx))
+            if q == 1:
+                dec_rows.append(start)
+                dec_tables.append(table)
+                dec_ctx.append(ctx)
+            else:
+                ch_rows.extend(range(start, start + q))
+                ch_tables.append(table)
+                ch_ctx.append(ctx)
+                ch_q.append(q)
+            start += q
+        qlens = torch.tensor(list(query_lens), device=device)
+        last = torch.cumsum(qlens, 0) - 1
+        batch = cls(cache=cache,
+                    slot_mapping=torch.tensor(slots, dtype=torch.int64, device=device),
+                    last_index=last, mixed=True)  # fmt: skip
+        if dec_rows:
+            batch.decode_rows = torch.tensor(dec_rows, dtype=torch.int64, device=device)
+            batch.block_tables = cls._tables(dec_tables).to(device)
+            batch.context_lens = torch.tensor(dec_ctx, dtype=torch.int32, device=device)
+        if ch_rows:
+            tables = cls._tables(ch_tables)
+            cu = torch.zeros(len(ch_q) + 1, dtype=torch.int32)
+            cu[1:] = torch.cumsum(torch.tensor(ch_q, dtype=torch.int32), 0)
+            batch.chunk_rows = torch.tensor(ch_rows, dtype=torch.int64, device=device)
+            batch.chunk_tables = tables.to(device)
+            batch.chunk_ctx = torch.tensor(ch_ctx, dtype=torch.int32, device=device)
+            batch.cu_seqlens_q = cu.to(device)
+            batch.max_query_len = max(ch_q)
+            owner = torch.repeat_interleave(torch.arange(len(ch_q)), torch.tensor(ch_q))
+            within = torch.cat([torch.arange(q) for q in ch_q])
+            batch.row_tables = tables[owner].to(device)
+            batch.row_ctx = (torch.tensor(ch_ctx)[owner] - torch.tensor(ch_q)[owner]
+                             + within + 1).to(torch.int32).to(device)  # fmt: skip
+        return batch

@@ -1,0 +1,225 @@
+"""End-to-end greedy-token identity through the paged path.
+
+CPU tests (torch-only "reference" attention backend) pin the harness itself: block
+tables, chunked prefill, prefix-cache hits, fork with copy-on-write and the
+``PagedBatch`` metadata must give the static loop's tokens. The GPU tests run the same
+engine on the HIP kernels (tests/test_kernels.py:40-179 of the reference is the
+pattern: engine tokens == static-loop tokens, graphs == eager, mixed steps)."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from engine.runtime.paged_cache import PagedBatch, PagedKVCache
+from tiny_llama import ReferenceBackend, TinyConfig, TinyEngine, TinyLlama, static_greedy
+
+SHARED = [7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18]
+PROMPTS = {"a": [5, 6, 7], "b": SHARED + [1, 2], "c": [99], "d": SHARED + [3],
+           "e": list(range(20, 41)), "f": SHARED}  # fmt: skip
+
+
+def _model(dtype=torch.float32, device="cpu", **cfg) -> TinyLlama:
+    torch.manual_seed(0)
+    return TinyLlama(TinyConfig(**cfg), seed=0).to(device=device, dtype=dtype).eval()
+
+
+def _oracle(model, prompts, max_tokens):
+    return {rid: static_greedy(model, p, max_tokens) for rid, p in prompts.items()}
+
+
+def _check_logits(eng, prompts, max_tokens, atol):
+    """Every sampled token's logits against the static loop's (same tokens assumed)."""
+    worst = 0.0
+    for rid, p in prompts.items():
+        _, want = static_greedy(eng.model, p, max_tokens, with_logits=True)
+        got = torch.stack(eng.logits[rid])
+        worst = max(worst, (got - want).abs().max().item())
+    assert worst <= atol, f"logits differ from the static loop by {worst}"
+    return worst
+
+
+def _run_staggered(eng: TinyEngine, prompts, max_tokens):
+    """Prompts join one per step while earlier ones decode: mixed steps."""
+    got = {rid: [] for rid in prompts}
+    pending = list(prompts.items())
+    while pending or eng.has_unfinished():
+        if pending:
+            rid, p = pending.pop(0)
+            eng.add_request(rid, p, max_tokens)
+        for rid, tok in eng.step():
+            got[rid].append(tok)
+    return got
+
+
+def test_paged_batch_metadata_matches_definitions():
+    """slot_mapping, chunk offsets and per-token causal contexts against their
+    definitions (reference engine/runtime/paged_cache.py:80-229)."""
+    cfg = TinyConfig()
+    cache = PagedKVCache(cfg, 40, 4, "cpu", torch.float32)
+    tables = [[3, 9, 1], [0], [5, 6, 7, 8], [2, 4]]
+    ctx = [10, 1, 13, 6]
+    qlen = [1, 1, 5, 6]  # two decode rows, a later chunk, a whole prompt
+    b = PagedBatch.build(cache, tables, ctx, qlen, "cpu")
+    assert b.mixed
+    want_slots = [t[p // 4] * 4 + p % 4 for t, n, q in zip(tables, ctx, qlen)
+                  for p in range(n - q, n)]  # fmt: skip
+    assert b.slot_mapping.tolist() == want_slots
+    assert b.last_index.tolist() == [0, 1, 6, 12]
+    assert b.decode_rows.tolist() == [0, 1]
+    assert b.context_lens.tolist() == [10, 1]
+    assert b.chunk_rows.tolist() == list(range(2, 13))
+    assert b.cu_seqlens_q.tolist() == [0, 5, 11] and b.max_query_len == 6
+    assert b.chunk_ctx.tolist() == [13, 6]
+    # Query i of a chunk of q tokens in a context of n sees keys 0 .. n - q + i.
+    assert b.row_ctx.tolist() == [9, 10, 11, 12, 13, 1, 2, 3, 4, 5, 6]
+    assert b.row_tables[0].tolist() == [5, 6, 7, 8] and b.row_tables[5].tolist()[:2] == [2, 4]
+    d = PagedBatch.build(cache, tables[:2], ctx[:2], [1, 1], "cpu")
+    assert not d.mixed and d.slot_mapping.tolist() == want_slots[:2]
+    assert d.block_tables.tolist() == [[3, 9, 1], [0, 0, 0]]  # padded with block 0
+    with pytest.raises(ValueError):
+        PagedBatch.build(cache, [[1]], [9], [2], "cpu")  # table too short
+    with pytest.raises(ValueError):
+        PagedBatch.build(cache, [[1]], [2], [1], "cpu", use_kernel=False)
+
+
+@pytest.mark.parametrize("budget", [4096, 8])
+def test_engine_reference_backend_matches_static_loop(budget):
+    model = _model()
+    want = _oracle(model, PROMPTS, 10)
+    eng = TinyEngine(model, ReferenceBackend(), num_blocks=64, block_size=4,
+                     max_num_batched_tokens=budget)  # fmt: skip
+    assert _run_staggered(eng, PROMPTS, 10) == want
+    _check_logits(eng, PROMPTS, 10, atol=1e-4)
+    assert any(not s["decode_only"] for s in eng.log) and any(s["decode_only"] for s in eng.log)
+    assert eng.bm.num_free_blocks == 64
+    # Prefix-cache hits happened ("b", "d", "f" share 12 tokens).
+    assert eng.bm.num_cached_blocks > 0
+
+
+def test_engine_fork_copy_on_write_reference_backend():
+    """A child forked mid-decode with a different pending token shares the parent's
+    partly filled last block; both must still match their own static loops."""
+    model = _model()
+    prompt = list(range(30, 41))  # 11 tokens: last block of 4 partly filled
+    eng = TinyEngine(model, ReferenceBackend(), num_blocks=32, block_size=4)
+    eng.add_request("p", prompt, 8)
+    for _ in range(3):  # prefill + 2 decodes -> 13 computed, 1 pending
+        eng.step()
+    parent = eng.running[0]
+    assert parent.num_computed == 13 and len(parent.out) == 3
+    forced = (parent.out[-1] + 1) % model.cfg.vocab_size
+    eng.fork("p", "c", next_token=forced)
+    while eng.has_unfinished():
+        eng.step()
+    assert sum(s["copies"] for s in eng.log) >= 1
+    _check_fork(eng, model, prompt, parent.out[:2], forced, atol=1e-4)
+    assert eng.bm.num_free_blocks == 32
+
+
+def _check_fork(eng, model, prompt, shared_out, forced, atol):
+    """Parent tokens and logits == static loop on the prompt; the child's tokens after
+    the fork and their logits == static loop on prompt + shared outputs + forced."""
+    want_p, logits_p = static_greedy(model, prompt, 8, with_logits=True)
+    assert eng.done["p"] == want_p
+    assert (torch.stack(eng.logits["p"]) - logits_p).abs().max().item() <= atol
+    want_c, logits_c = static_greedy(model, prompt + shared_out + [forced], 5,
+                                     with_logits=True)  # fmt: skip
+    assert eng.done["c"] == shared_out + [forced] + want_c
+    got_c = torch.stack(eng.logits["c"][3:])
+    assert (got_c - logits_c).abs().max().item() <= atol
+
+
+# --- GPU: the same engine on the HIP kernels ----------------------------------------
+
+
+def _cuda_model(dtype, **cfg):
+    return _model(dtype=dtype, device="cuda", **cfg)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("budget", [4096, 8])
+def test_engine_kernels_match_static_loop_fp32(budget):
+    """fp32: decode kernel (fp32 instantiation) and, for prompt chunks, the decode kernel
+    per chunk token. Tokens and logits == the static loop."""
+    from tiny_llama import KernelBackend
+
+    model = _cuda_model(torch.float32)
+    want = _oracle(model, PROMPTS, 10)
+    eng = TinyEngine(model, KernelBackend(), num_blocks=64, block_size=4,
+                     max_num_batched_tokens=budget)  # fmt: skip
+    assert _run_staggered(eng, PROMPTS, 10) == want
+    _check_logits(eng, PROMPTS, 10, atol=2e-4)
+    assert eng.bm.num_free_blocks == 64 and eng.bm.num_cached_blocks > 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize(("hd", "bs"), [(64, 4), (128, 16)])
+def test_engine_kernels_match_reference_backend_16bit(dtype, hd, bs):
+    """16-bit: decode kernel + MFMA chunked-prefill kernel against the same engine on the
+    reference's gather-then-attention (fp32 math, rounded to the model dtype), on the
+    same flattened steps: identical tokens, logits within rounding."""
+    from tiny_llama import KernelBackend
+
+    model = _cuda_model(dtype, hidden_size=4 * hd, num_attention_heads=4,
+                        num_key_value_heads=2)  # fmt: skip
+    runs = {}
+    for backend in (ReferenceBackend(), KernelBackend()):
+        eng = TinyEngine(model, backend, num_blocks=64, block_size=bs,
+                         max_num_batched_tokens=8)  # fmt: skip
+        runs[backend.name] = (_run_staggered(eng, PROMPTS, 10), eng)
+    assert runs["kernel"][0] == runs["reference"][0]
+    worst = max((torch.stack(runs["kernel"][1].logits[r]) -
+                 torch.stack(runs["reference"][1].logits[r])).abs().max().item()
+                for r in PROMPTS)  # fmt: skip
+    assert worst <= 0.05, worst  # 16-bit activations: a few ulps of the logits
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_decode_graphs_match_eager(dtype):
+    """Decode steps replayed from hipGraphs (slot mapping built on the device, padding
+    rows on the scratch block) give the eager engine's tokens and logits."""
+    from tiny_llama import KernelBackend
+
+    model = _cuda_model(dtype)
+    prompts = dict(list(PROMPTS.items())[:3])  # three sequences pad to the 4-bucket
+    runs = {}
+    for graphs in (False, True):
+        eng = TinyEngine(model, KernelBackend(), num_blocks=64, block_size=4, max_num_seqs=8,
+                         graphs=graphs)  # fmt: skip
+        runs[graphs] = (eng.generate(prompts, 30), eng)
+    assert runs[True][0] == runs[False][0]
+    assert sum(s["graph"] for s in runs[True][1].log) >= 20
+    # Padding to the bucket changes only the GEMM row count: rounding-level differences.
+    atol = 1e-4 if dtype == torch.float32 else 0.05
+    for r in prompts:
+        diff = torch.stack(runs[True][1].logits[r]) - torch.stack(runs[False][1].logits[r])
+        assert diff.abs().max().item() <= atol, r
+    if dtype == torch.float32:
+        assert runs[True][0] == _oracle(model, prompts, 30)
+    assert runs[True][1].bm.num_free_blocks == 64
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("graphs", [False, True])
+def test_engine_fork_copy_on_write_kernels(graphs):
+    """Fork mid-decode on the HIP path: copy_blocks gives the child its own copy of the
+    shared partly filled block before the append; both match their static loops."""
+    from tiny_llama import KernelBackend
+
+    model = _cuda_model(torch.float32)
+    prompt = list(range(30, 41))
+    eng = TinyEngine(model, KernelBackend(), num_blocks=32, block_size=4, graphs=graphs)
+    eng.add_request("p", prompt, 8)
+    for _ in range(3):
+        eng.step()
+    parent = eng.running[0]
+    forced = (parent.out[-1] + 1) % model.cfg.vocab_size
+    eng.fork("p", "c", next_token=forced)
+    while eng.has_unfinished():
+        eng.step()
+    assert sum(s["copies"] for s in eng.log) >= 1
+    _check_fork(eng, model, prompt, parent.out[:2], forced, atol=2e-4)
+    assert eng.bm.num_free_blocks == 32

@@ -16,7 +16,7 @@ import torch
 from engine import workloads
 from engine.kernels import _native
 from engine.kernels import paged_attention as pa
-from engine.runtime.paged_cache import PagedKVCache, KVShape, copy_blocks, kv_append
+from engine.runtime.paged_cache import PagedKVCache, KVShape, copy_blocks, decode_slots, kv_append
 from oracle import oracle
 
 pytestmark = pytest.mark.gpu
@@ -378,6 +378,33 @@ def test_workspace_reuse_and_garbage(wgs):
     for o in outs[1:]:
         assert torch.equal(_bits(o), _bits(outs[0]))
     _check_attention(step, wgs=wgs, what=f"ws{wgs}")
+
+
+@pytest.mark.parametrize("bs", [16, 4, 3])
+def test_decode_slots_on_device(bs):
+    """The device slot builder against the host formula of PagedBatch._decode
+    (reference engine/runtime/paged_cache.py:140-143), with graph-style tables (row
+    stride > W), padding rows (ctx 1), and the cases it must map to -1: ctx < 1, a block
+    past the table, a block id outside the pool."""
+    _say("decode_slots", bs)
+    g = torch.Generator().manual_seed(bs)
+    b, w, nblk = 37, 9, 50
+    full = torch.randint(0, nblk, (b, w + 3), generator=g, dtype=torch.int32)
+    tables = full[:, :w]
+    ctx = torch.randint(1, w * bs + 1, (b,), generator=g, dtype=torch.int32)
+    ctx[0], ctx[1], ctx[2] = 0, -5, w * bs + 1  # no token; negative; past the table
+    ctx[3] = 1  # a graph padding row
+    tables[4, (int(ctx[4]) - 1) // bs] = nblk + 7  # outside the pool
+    want = []
+    for i in range(b):
+        n = int(ctx[i])
+        blk = (n - 1) // bs if n >= 1 else -1
+        s_ = int(tables[i, blk]) * bs + (n - 1) % bs if 0 <= blk < w else -1
+        want.append(s_ if 0 <= s_ < nblk * bs else -1)
+    got = decode_slots(full.to(DEV)[:, :w], ctx.to(DEV), bs, nblk * bs)
+    torch.cuda.synchronize()
+    assert got.cpu().tolist() == want
+    assert want[0] == want[1] == want[2] == want[4] == -1 and want[3] >= 0
 
 
 def test_native_library_is_loaded_from_tree():
