@@ -1085,7 +1085,8 @@ struct PrefillArgs {
   const int32_t* ctx;   // [n_chunks] context tokens (the chunk's own included)
   const int32_t* cu_q;  // [n_chunks + 1] query row offsets
   int32_t n_chunks, nh, nkv, groups, bs, bs_shift;
-  int32_t row_blocks;   // grid.x: 128-row blocks per chunk (static bound)
+  int32_t row_blocks;   // 128-row blocks per chunk (static bound)
+  int32_t pair_halves;  // the whole grid is resident at once: pair heavy with light items
   float scale_log2;
   int out_f32;
 };
@@ -1201,13 +1202,15 @@ template <int HD> struct PrefillShape {
   static_assert(NLD >= 1 && KT * CH % 256 == 0, "tile must split evenly over 256 threads");
   static_assert(2 * NLD < 64, "vmcnt range");
   static_assert(KT <= kWave, "a tile's block ids must fit one 64-entry table window");
-  // LDS position of chunk c of key t's row is c ^ swz(t). With 16 chunks per row (head
-  // dim 128) swz rotates the token's low 4 bits left by one: the K operand reads (16
-  // consecutive keys, one chunk) and the V^T transpose reads (8 consecutive keys, chunks
-  // 2d and 2d + 1) then both hit distinct banks; a plain t % 16 makes keys x and x ^ 1
-  // collide in the transpose reads.
+  // LDS position of chunk c of key t's row is c ^ swz(t). Rows are 256 bytes (head dim
+  // 128, 16 chunks), so a chunk's bank group is its position mod 8 (a 128-byte access
+  // window). The K operand reads (ds_read_b128: 8 lanes = 8 consecutive keys, one chunk,
+  // per access) are conflict-free when swz's low 3 bits are a bijection of the key's low
+  // 3 bits; the V^T transpose reads (4 consecutive keys x chunks 2d, 2d + 1 per 16
+  // lanes) when swz's bits 1-2 are a bijection of the key's bits 0-1. swz(t) = (t2, t0,
+  // t1, t3) -- bits 0..3 -- satisfies both.
   __device__ static int swz(int t) {
-    if constexpr (CH == 16) return ((t << 1) | ((t >> 3) & 1)) & 15;
+    if constexpr (CH == 16) return ((t << 1) & 6) | ((t >> 2) & 1) | (t & 8);
     else return t % CH;
   }
 };
@@ -1231,12 +1234,23 @@ paged_prefill_kernel(const PrefillArgs a) {
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int col = lane & 15, grp = lane >> 4;
-  const int kvh = blockIdx.y;
-
-  // Chunks are taken longest context first (blockIdx.z = rank), and inside a chunk the
-  // last row blocks (which see the most keys) first, so the longest workgroups start
-  // earliest. Each wave ranks up to 64 chunks by itself; larger batches keep their order.
-  int c = blockIdx.z;
+  // Work items (chunk, row block, KV head), heaviest first: chunks by context length
+  // (longest first), then row blocks from the last (it sees the most keys), KV heads
+  // innermost. A grid larger than the GPU holds runs them in that order, so the longest
+  // items start earliest. When the whole grid is resident at once, workgroups L and
+  // L + N/2 are dealt to the same CU, so the second half takes the items in reverse:
+  // each CU then holds the k-th heaviest and the k-th lightest item.
+  const int nitems = (int)gridDim.x;
+  int item = (int)blockIdx.x;
+  if (a.pair_halves) {
+    const int half = (nitems + 1) / 2;
+    if (item >= half) item = nitems - 1 - (item - half);
+  }
+  const int kvh = item % a.nkv;
+  const int rbi = (item / a.nkv) % a.row_blocks;
+  const int crank = item / (a.nkv * a.row_blocks);
+  // Each wave ranks up to 64 chunks by itself; larger batches keep their order.
+  int c = crank;
   if (a.n_chunks <= kWave) {
     const int cap0 = a.max_blocks * a.bs;
     const int mine = lane < a.n_chunks ? min(max(a.ctx[lane], 0), cap0) : -1;
@@ -1245,13 +1259,13 @@ paged_prefill_kernel(const PrefillArgs a) {
       const int other = __shfl(mine, j);
       rank += (other > mine) || (other == mine && j < lane);
     }
-    const uint64_t hit = __ballot(lane < a.n_chunks && rank == (int)blockIdx.z);
+    const uint64_t hit = __ballot(lane < a.n_chunks && rank == crank);
     c = __builtin_ctzll(hit);
   }
   const int q0 = a.cu_q[c], qlen = a.cu_q[c + 1] - q0;
   const int G = a.groups;
   const int nrows = qlen * G;
-  const int rho0 = (a.row_blocks - 1 - (int)blockIdx.x) * BM;
+  const int rho0 = (a.row_blocks - 1 - rbi) * BM;
   if (qlen <= 0 || rho0 >= nrows) return;  // uniform per workgroup
   const int cap = a.max_blocks * a.bs;
   const int n = min(max(a.ctx[c], 0), cap);
@@ -1729,7 +1743,18 @@ template <int DT, int HD>
 hipError_t launch_prefill_hd(PrefillArgs a, int64_t rows, hipStream_t st) {
   constexpr int BM = PrefillShape<HD>::BM;
   a.row_blocks = (int)((rows + BM - 1) / BM);
-  const dim3 grid((unsigned)a.row_blocks, (unsigned)a.nkv, (unsigned)a.n_chunks), block(256);
+  const int64_t items = (int64_t)a.row_blocks * a.nkv * a.n_chunks;
+  if (items > 0x7FFFFFFF) return hipErrorInvalidValue;
+  const void* kern = a.bs_shift >= 0 ? (const void*)&paged_prefill_kernel<DT, HD, true>
+                                     : (const void*)&paged_prefill_kernel<DT, HD, false>;
+  // Resident capacity (CUs x workgroups per CU) decides whether the halves pair up.
+  int dev = 0, cus = 0, per_cu = 0;
+  a.pair_halves = 0;
+  if (hipGetDevice(&dev) == hipSuccess &&
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, 0) == hipSuccess)
+    a.pair_halves = items <= (int64_t)cus * per_cu ? 1 : 0;
+  const dim3 grid((unsigned)items), block(256);
   if (a.bs_shift >= 0)
     hipLaunchKernelGGL((paged_prefill_kernel<DT, HD, true>), grid, block, 0, st, a);
   else
@@ -1997,6 +2022,7 @@ int pkv_paged_prefill(void* out, int out_dtype, int64_t out_stride_tok, int64_t 
   a.bs = block_size;
   a.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz(block_size) : -1;
   a.row_blocks = 0;  // set per head_dim by launch_prefill
+  a.pair_halves = 0;
   a.scale_log2 = scale * 1.4426950408889634f;
   a.out_f32 = out_dtype == PKV_F32;
   hipStream_t st = (hipStream_t)stream;

@@ -83,15 +83,9 @@ def test_prefill_groups_and_block_sizes(nh, nkv, bs):
     assert (got - want).abs().max().item() <= ATOL
 
 
-def test_prefill_config5_chunks_first_and_last_tokens():
-    """Config 5's prompt chunks (Llama-3-8B shape): 4 chunks of 512 tokens after cached
-    prefixes of 0, 1024, 2048, 3072 tokens. The oracle checks each chunk's first and
-    last 16 query tokens (as their own sub-chunks with the same visible keys)."""
-    _say("prefill config5")
-    bs, nh, nkv, hd = 16, 32, 8, 128
-    spec = [(512, 512 + 1024 * i) for i in range(4)]
-    q, k, v, tables, ctx, cu = _chunks(spec, nh, nkv, hd, bs, torch.bfloat16, seed=5)
-    got = _run(q, k, v, tables, ctx, cu, bs, 512)
+def _check_first_last(spec, q, k, v, tables, cu, got, bs):
+    """The oracle on each chunk's first and last 16 query tokens (as their own sub-chunks
+    with the same visible keys)."""
     for part in ("first", "last"):
         rows, sub_ctx, sub_cu = [], [], [0]
         for c, (ql, n) in enumerate(spec):
@@ -106,6 +100,29 @@ def test_prefill_config5_chunks_first_and_last_tokens():
                                         threads=THREADS)  # fmt: skip
         err = (got[rows] - want).abs().max().item()
         assert err <= ATOL, (part, err)
+
+
+def test_prefill_config5_chunks_first_and_last_tokens():
+    """Config 5's prompt chunks (Llama-3-8B shape): 4 chunks of 512 tokens after cached
+    prefixes of 0, 1024, 2048, 3072 tokens (512 work items: the whole grid is resident,
+    heavy and light items share CUs)."""
+    _say("prefill config5")
+    bs, nh, nkv, hd = 16, 32, 8, 128
+    spec = [(512, 512 + 1024 * i) for i in range(4)]
+    q, k, v, tables, ctx, cu = _chunks(spec, nh, nkv, hd, bs, torch.bfloat16, seed=5)
+    got = _run(q, k, v, tables, ctx, cu, bs, 512)
+    _check_first_last(spec, q, k, v, tables, cu, got, bs)
+
+
+def test_prefill_grid_larger_than_the_gpu():
+    """Two 2,048-token chunks at the Llama-3-8B shape: 1,024 work items, more than the
+    GPU holds at once, so they run heaviest first instead of paired."""
+    _say("prefill long chunks")
+    bs, nh, nkv, hd = 16, 32, 8, 128
+    spec = [(2048, 2048), (2048, 2560)]
+    q, k, v, tables, ctx, cu = _chunks(spec, nh, nkv, hd, bs, torch.bfloat16, seed=6)
+    got = _run(q, k, v, tables, ctx, cu, bs, 2048)
+    _check_first_last(spec, q, k, v, tables, cu, got, bs)
 
 
 def test_prefill_whole_prompt_is_causal_attention():
