@@ -18,7 +18,9 @@ graph-replay time per layer-step. ``cpu_baseline`` times the C oracle on host co
 
 ``--config c5`` measures the mixed chunked-prefill step of config 5 instead (append of
 2,168 rows, MFMA prefill of 4 x 512-token chunks, decode of 120 sequences); its line
-reports the prefill's TFLOP/s against the bf16 MFMA peak.
+reports the prefill's TFLOP/s against the bf16 MFMA peak and the append's GB/s.
+``--config c3`` adds the copy-on-write of the config's 64 block pairs across a 28-layer
+pool (``cow_*``: algorithmic bytes, and unique bytes with the shared source once).
 """
 
 from __future__ import annotations
@@ -216,9 +218,35 @@ def bench_decode(args, torch) -> dict:
     if step.cow_mapping is not None:
         line["unique_kv_bytes_per_step"] = step.unique_kv_bytes()
         line["unique_gbps"] = round(line["unique_kv_bytes_per_step"] / (value * 1e-6) / 1e9, 1)
+        line.update(bench_cow(torch, step))
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(step, args.cpu_seconds)
     return line
+
+
+def bench_cow(torch, step, layers: int = 28, blocks: int = 2048) -> dict:
+    """Copy-on-write of the step's pairs across a whole model's pool (28 layers, the
+    3B depth): every pair copies one 16-token block of every layer, K and V."""
+    from engine.runtime.paged_cache import copy_blocks
+
+    bs = step.block_size
+    _, nkv, hd = step.k_cache.shape
+    kp = torch.empty(layers, blocks * bs, nkv, hd, dtype=step.k_cache.dtype,
+                     device=step.k_cache.device)  # fmt: skip
+    vp = torch.empty_like(kp)
+    pairs = step.cow_mapping.shape[0]
+    mapping = torch.stack([torch.full((pairs,), 3, dtype=torch.int64),
+                           torch.arange(pairs, dtype=torch.int64) + 100], 1).to(kp.device)  # fmt: skip
+    us = graph_us(torch, [lambda: copy_blocks(kp, vp, mapping, bs)] * 8, 400, 16)[0]
+    blk = bs * nkv * hd * kp.element_size()
+    moved = 2 * pairs * layers * blk * 2  # K+V, every pair read + written
+    # config 3 copies one shared block to every destination: its reads hit the cache
+    srcs = int(torch.unique(mapping[:, 0]).numel())
+    unique = 2 * layers * blk * (srcs + pairs)
+    return {"cow_pairs": pairs, "cow_layers": layers, "cow_us": round(us, 2),
+            "cow_bytes": moved, "cow_gbps": round(moved / (us * 1e-6) / 1e9, 1),
+            "cow_unique_bytes": unique,
+            "cow_unique_gbps": round(unique / (us * 1e-6) / 1e9, 1)}
 
 
 def bench_mixed(args, torch) -> dict:
@@ -255,6 +283,8 @@ def bench_mixed(args, torch) -> dict:
     flops = m.prefill_flops()
     tflops = flops / (t_pre * 1e-6) / 1e12
     dec_gbps = d.kv_bytes() / (t_dec * 1e-6) / 1e9
+    # append: every new row read once and written once, K and V
+    app_bytes = 2 * m.new_k.numel() * m.new_k.element_size() * 2
     return {
         "metric": "mixed chunked-prefill layer-step us (config 5)",
         "value": round(step_us, 2),
@@ -284,6 +314,8 @@ def bench_mixed(args, torch) -> dict:
         "decode_us": round(t_dec, 2),
         "decode_gbps": round(dec_gbps, 1),
         "append_us": round(t_app, 2),
+        "append_bytes": app_bytes,
+        "append_gbps": round(app_bytes / (t_app * 1e-6) / 1e9, 1),
         "timed_wall_s": round(wall, 4),
     }
 

@@ -223,3 +223,33 @@ def test_engine_fork_copy_on_write_kernels(graphs):
     assert sum(s["copies"] for s in eng.log) >= 1
     _check_fork(eng, model, prompt, parent.out[:2], forced, atol=2e-4)
     assert eng.bm.num_free_blocks == 32
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("budget", [4096, 8])
+def test_mixed_graphs_match_eager(dtype, budget):
+    """Mixed steps replayed as one hipGraph per token bucket (prompts joining while
+    others decode, chunked under budget 8, prefix-cache hits) give the eager engine's
+    tokens; in fp32 also the static loop's. Decode-only steps use DecodeGraphs."""
+    from tiny_llama import KernelBackend
+
+    model = _cuda_model(dtype)
+    prompts = dict(PROMPTS, g=list(range(50, 90)))
+    runs = {}
+    for graphs in (False, True):
+        eng = TinyEngine(model, KernelBackend(), num_blocks=64, block_size=4, max_num_seqs=8,
+                         max_num_batched_tokens=budget, graphs=graphs,
+                         mixed_graphs=graphs)  # fmt: skip
+        runs[graphs] = (_run_staggered(eng, prompts, 12), eng)
+        assert eng.bm.num_free_blocks == 64
+    assert runs[True][0] == runs[False][0]
+    log = runs[True][1].log
+    assert sum(s["mixed_graph"] for s in log) >= 3 and sum(s["graph"] for s in log) >= 3
+    assert not any(s["mixed_graph"] or s["graph"] for s in runs[False][1].log)
+    atol = 1e-4 if dtype == torch.float32 else 0.05
+    for r in prompts:
+        diff = torch.stack(runs[True][1].logits[r]) - torch.stack(runs[False][1].logits[r])
+        assert diff.abs().max().item() <= atol, r
+    if dtype == torch.float32:
+        assert runs[True][0] == _oracle(model, prompts, 12)

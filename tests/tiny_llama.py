@@ -249,7 +249,7 @@ class TinyEngine:
     def __init__(self, model: TinyLlama, backend, num_blocks: int = 64, block_size: int = 4,
                  max_num_seqs: int = 8, max_num_batched_tokens: int = 4096,
                  enable_prefix_caching: bool = True, graphs: bool = False,
-                 debug_checks: bool = True) -> None:  # fmt: skip
+                 mixed_graphs: bool = False, debug_checks: bool = True) -> None:  # fmt: skip
         self.model, self.backend = model, backend
         w = model.embed.weight
         self.device, self.dtype = w.device, w.dtype
@@ -271,6 +271,12 @@ class TinyEngine:
 
             self.graphs = DecodeGraphs(model, self.cache, num_blocks, max_num_seqs,
                                        num_blocks)  # fmt: skip
+        self.mixed_graphs = None
+        if mixed_graphs:
+            from engine.runtime.cuda_graphs import MixedGraphs
+
+            self.mixed_graphs = MixedGraphs(model, self.cache, num_blocks, max_num_seqs,
+                                            max_num_batched_tokens, num_blocks)  # fmt: skip
 
     def add_request(self, rid: str, prompt: list[int], max_tokens: int) -> None:
         self.waiting.append(Seq(rid, self._next_id, list(prompt), len(prompt), max_tokens))
@@ -333,11 +339,16 @@ class TinyEngine:
             self.backend.copy(self.cache, torch.tensor(pairs, dtype=torch.int64,
                                                        device=self.device))  # fmt: skip
         decode_only = max(qlens) == 1
-        used_graph = False
-        if self.graphs is not None and decode_only and \
-                self.graphs.can_run(len(plan), max(len(t) for t in tables)):  # fmt: skip
+        width = max(len(t) for t in tables)
+        used_graph = used_mixed_graph = False
+        if self.graphs is not None and decode_only and self.graphs.can_run(len(plan), width):
             logits = self.graphs.run(ids, positions, None, tables, ctx)[:, 0]
             used_graph = True
+        elif self.mixed_graphs is not None and not decode_only and \
+                self.mixed_graphs.can_run(len(ids), len(plan), width):  # fmt: skip
+            batch = PagedBatch.build(self.cache, tables, ctx, qlens, self.device)
+            logits = self.mixed_graphs.run(ids, positions, batch)[:, 0]
+            used_mixed_graph = True
         else:
             batch = PagedBatch.build(self.cache, tables, ctx, qlens, self.device)
             logits = self.model(torch.tensor([ids], device=self.device),
@@ -361,7 +372,8 @@ class TinyEngine:
         if self.debug_checks:
             self.bm.check_no_leaks()
         self.log.append({"seqs": len(plan), "tokens": len(ids), "decode_only": decode_only,
-                         "graph": used_graph, "copies": len(pairs)})  # fmt: skip
+                         "graph": used_graph, "mixed_graph": used_mixed_graph,
+                         "copies": len(pairs)})  # fmt: skip
         return outputs
 
     def generate(self, prompts: dict[str, list[int]], max_tokens: int) -> dict[str, list[int]]:
