@@ -152,6 +152,41 @@ int pkv_paged_prefill(void* out, int out_dtype, int64_t out_stride_tok, int64_t 
                       int32_t max_query_len, int32_t num_heads, int32_t num_kv_heads,
                       int32_t head_dim, int32_t block_size, float scale, void* stream);
 
+/*
+ * Fused element-wise kernels (csrc/fused.hip). Replace the reference's Triton kernels of
+ * engine/kernels/fused.py:47-131 (rms_norm, rope_, silu_mul), with the same contract:
+ * every result is bitwise identical to the PyTorch ops they stand for.
+ *
+ * RMSNorm tail (reference fused.py:47-59, :93-111): for row r and column c,
+ *   out[r, c] = w[c] * (x[r, c] (as fp32) * inv_rms[r]).to(x dtype)
+ * inv_rms (fp32 [rows]) = rsqrt(mean(x[r]^2) + eps) is computed by the caller with
+ * PyTorch: the reference leaves the mean to PyTorch (a fused sum adds in another order),
+ * and PyTorch's ROCm rsqrt can differ from the device library's in the last fp32 bit.
+ * out_dtype must be the promotion of x_dtype and w_dtype (equal dtypes stay; mixed ones
+ * give PKV_F32). Columns are unit-stride.
+ */
+int pkv_rms_norm(void* out, int out_dtype, int64_t out_stride_row, const void* x, int x_dtype,
+                 int64_t x_stride_row, const float* inv_rms, const void* weight, int w_dtype,
+                 int64_t rows, int64_t cols, void* stream);
+
+/*
+ * RoPE in place (reference fused.py:61-80, :114-121): x [n_tokens, heads, head_dim]
+ * (unit stride in head_dim) becomes x * cos + rotate_half(x) * sin, rotate_half(x) =
+ * cat(-x[half:], x[:half]); cos / sin are fp32 [n_tokens, head_dim] with row stride
+ * cs_stride_tok, cast to x's dtype first; each product and the sum round to the dtype.
+ */
+int pkv_rope(void* x, int dtype, int64_t stride_tok, int64_t stride_head, const float* cos,
+             const float* sin, int64_t cs_stride_tok, int64_t n_tokens, int32_t heads,
+             int32_t head_dim, void* stream);
+
+/*
+ * SiLU and multiply (reference fused.py:82-90, :124-131): out = silu(gate) * up, silu
+ * computed in fp32 as g / (1 + exp(-g)) and rounded to the dtype, then the product
+ * rounded. gate, up, out: n contiguous elements of one dtype.
+ */
+int pkv_silu_mul(void* out, const void* gate, const void* up, int dtype, int64_t n,
+                 void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -2,10 +2,10 @@
 
     python inference-engine_amd/csrc/build.py
 
-compiles csrc/paged_kv.hip with hipcc for gfx950 into lib/libpaged_kv.so (next to the
-engine package). The library links libamdhip64.so.7; loaded after ``import torch`` it
-binds to the HIP runtime torch already loaded (same SONAME), so torch's streams and
-device pointers are valid inside it.
+compiles csrc/paged_kv.hip and csrc/fused.hip with hipcc for gfx950 into
+lib/libpaged_kv.so (next to the engine package). The library links libamdhip64.so.7;
+loaded after ``import torch`` it binds to the HIP runtime torch already loaded (same
+SONAME), so torch's streams and device pointers are valid inside it.
 """
 
 from __future__ import annotations
@@ -20,7 +20,7 @@ PKG_ROOT = os.path.dirname(HERE)
 REPO = os.path.dirname(PKG_ROOT)
 LIB_DIR = os.path.join(PKG_ROOT, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libpaged_kv.so")
-SOURCES = [os.path.join(HERE, "paged_kv.hip")]
+SOURCES = [os.path.join(HERE, "paged_kv.hip"), os.path.join(HERE, "fused.hip")]
 INCLUDE = os.path.join(REPO, "include")
 
 HIPCC_FLAGS = [

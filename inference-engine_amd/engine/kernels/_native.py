@@ -46,6 +46,12 @@ SIGNATURES: dict[str, tuple] = {
          _p, _i32, _i32, _i32, _i32, _i32,        # ctx, batch, nh, nkv, hd, bs
          _f32, _i32, _p, _i64, _p],               # scale, wgs, workspace, stream
     ),  # fmt: skip
+    "pkv_rms_norm": (
+        ctypes.c_int,
+        [_p, ctypes.c_int, _i64, _p, ctypes.c_int, _i64, _p, _p, ctypes.c_int, _i64, _i64, _p],
+    ),  # fmt: skip
+    "pkv_rope": (ctypes.c_int, [_p, ctypes.c_int, _i64, _i64, _p, _p, _i64, _i64, _i32, _i32, _p]),
+    "pkv_silu_mul": (ctypes.c_int, [_p, _p, _p, ctypes.c_int, _i64, _p]),
     "pkv_paged_prefill": (
         ctypes.c_int,
         [_p, ctypes.c_int, _i64, _i64,            # out

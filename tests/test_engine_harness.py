@@ -253,3 +253,23 @@ def test_mixed_graphs_match_eager(dtype, budget):
         assert diff.abs().max().item() <= atol, r
     if dtype == torch.float32:
         assert runs[True][0] == _oracle(model, prompts, 12)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_fused_elementwise_kernels_change_nothing(dtype):
+    """RMSNorm, RoPE and SiLU x up on the fused HIP kernels: every logit of every step is
+    bitwise the same as with the PyTorch ops (reference engine/kernels/fused.py's
+    contract), through chunked prefill, decode and graph replays."""
+    from tiny_llama import KernelBackend
+
+    runs = {}
+    for use in (False, True):
+        model = _cuda_model(dtype).use_fused(use)
+        eng = TinyEngine(model, KernelBackend(), num_blocks=64, block_size=4,
+                         max_num_batched_tokens=8, graphs=True, mixed_graphs=True)  # fmt: skip
+        runs[use] = (_run_staggered(eng, PROMPTS, 10), eng)
+    assert runs[True][0] == runs[False][0]
+    for r in PROMPTS:
+        assert torch.equal(torch.stack(runs[True][1].logits[r]),
+                           torch.stack(runs[False][1].logits[r])), r  # fmt: skip

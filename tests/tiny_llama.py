@@ -54,7 +54,13 @@ class RMSNorm(nn.Module):
         self.weight = nn.Parameter(torch.ones(n))
         self.eps = eps
 
+    fused = False  # engine.kernels.fused (HIP) instead of the PyTorch ops
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self.fused:
+            from engine.kernels import fused
+
+            return fused.rms_norm(x, self.weight, self.eps)
         xf = x.float()
         y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
         return self.weight * y.to(x.dtype)
@@ -97,24 +103,45 @@ class TinyLlama(nn.Module):
                     p.copy_(torch.randn(p.shape, generator=g) / math.sqrt(p.shape[-1]))
             self.embed.weight.mul_(math.sqrt(cfg.hidden_size))
         self.attend = None  # (layer_idx, q, k, v, batch) -> [N, nh * hd], set by the engine
+        self.fused = False  # RMSNorm / RoPE / SiLU x up on engine.kernels.fused (HIP)
+
+    def use_fused(self, on: bool = True) -> TinyLlama:
+        """The fused HIP kernels for RMSNorm, RoPE and SiLU x up: bitwise the same as the
+        PyTorch ops, so every output must stay identical."""
+        self.fused = on
+        for m in self.modules():
+            if isinstance(m, RMSNorm):
+                m.fused = on
+        return self
 
     def rope(self, positions: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        """cos, sin [T, hd] in float32 (cast to the model dtype where they are used)."""
         hd = self.cfg.head_dim
         freqs = torch.arange(0, hd, 2, device=positions.device).float() / hd
         inv = 1.0 / self.cfg.rope_theta**freqs
         ang = positions.float()[:, None] * inv[None]
         ang = torch.cat([ang, ang], dim=-1)
-        dt = self.embed.weight.dtype
-        return ang.cos().to(dt), ang.sin().to(dt)
+        return ang.cos(), ang.sin()
 
     def _qkv(self, layer: Layer, x: torch.Tensor, cos, sin):
         t, hd = x.shape[0], self.cfg.head_dim
-        q = rotate(layer.q(x).view(t, -1, hd), cos, sin)
-        k = rotate(layer.k(x).view(t, -1, hd), cos, sin)
+        q, k = layer.q(x).view(t, -1, hd), layer.k(x).view(t, -1, hd)
+        if self.fused:
+            from engine.kernels import fused
+
+            fused.rope_(q, cos, sin)
+            fused.rope_(k, cos, sin)
+        else:
+            dt = x.dtype
+            q, k = rotate(q, cos.to(dt), sin.to(dt)), rotate(k, cos.to(dt), sin.to(dt))
         return q, k, layer.v(x).view(t, -1, hd)
 
     def _mlp(self, layer: Layer, h: torch.Tensor) -> torch.Tensor:
         y = layer.norm2(h)
+        if self.fused:
+            from engine.kernels import fused
+
+            return h + layer.down(fused.silu_mul(layer.gate(y), layer.up(y)))
         return h + layer.down(F.silu(layer.gate(y)) * layer.up(y))
 
     @torch.inference_mode()
