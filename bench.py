@@ -20,7 +20,8 @@ graph-replay time per layer-step. ``cpu_baseline`` times the C oracle on host co
 2,168 rows, MFMA prefill of 4 x 512-token chunks, decode of 120 sequences); its line
 reports the prefill's TFLOP/s against the bf16 MFMA peak and the append's GB/s.
 ``--config c3`` adds the copy-on-write of the config's 64 block pairs across a 28-layer
-pool (``cow_*``: algorithmic bytes, and unique bytes with the shared source once).
+pool (``cow_*``: algorithmic bytes, and unique bytes with the shared source once) and the
+same decode with cascade over the shared prefix (``cascade_*``, GB/s on unique bytes).
 """
 
 from __future__ import annotations
@@ -219,9 +220,34 @@ def bench_decode(args, torch) -> dict:
         line["unique_kv_bytes_per_step"] = step.unique_kv_bytes()
         line["unique_gbps"] = round(line["unique_kv_bytes_per_step"] / (value * 1e-6) / 1e9, 1)
         line.update(bench_cow(torch, step))
+        line.update(bench_cascade(args, torch, step, pools, out, wgs,
+                                  line["unique_kv_bytes_per_step"]))  # fmt: skip
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(step, args.cpu_seconds)
     return line
+
+
+def bench_cascade(args, torch, step, pools, out, wgs, unique_bytes) -> dict:
+    """The same layer-steps with cascade decode: prefix groups found from the block
+    tables (once per step, on the host), each shared prefix read once per group."""
+    from engine.kernels import paged_attention as pa
+
+    nh, nkv = step.q.shape[1], step.k_cache.shape[1]
+    pg = pa.find_prefix_groups(step.block_tables.cpu(), step.context_lens.cpu(),
+                               step.block_size, nh, nkv, step.q.device)  # fmt: skip
+    if pg is None:
+        return {"cascade": None}
+
+    def fn(k, v):
+        return lambda: pa.paged_decode_attention(
+            step.q, k, v, step.block_tables, step.context_lens, step.block_size, out=out,
+            num_workgroups=wgs, prefix_groups=pg)  # fmt: skip
+
+    us = graph_us(torch, [fn(k, v) for k, v in pools], args.steps, args.warmup)[0]
+    gbps = unique_bytes / (us * 1e-6) / 1e9
+    return {"cascade_us": round(us, 2), "cascade_unique_gbps": round(gbps, 1),
+            "cascade_unique_frac": round(gbps / HBM_PEAK_GBPS, 4),
+            "cascade_groups": int(pg.ctx.numel() // pg.pieces), "cascade_pieces": pg.pieces}
 
 
 def bench_cow(torch, step, layers: int = 28, blocks: int = 2048) -> dict:

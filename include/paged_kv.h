@@ -127,6 +127,42 @@ int pkv_paged_decode(void* out, int out_dtype, int64_t out_stride_b, int64_t out
                      int64_t workspace_bytes, void* stream);
 
 /*
+ * pkv_paged_decode with two optional extras, for cascade decode over shared prefixes
+ * (no counterpart in the reference, which reads every sequence's whole context):
+ *   first_block (int32 [batch], or NULL = all 0): sequence b attends only to table columns
+ *     first_block[b] onwards, i.e. to positions first_block[b] * block_size .. n - 1 (a
+ *     shared prefix held in the earlier columns is handled by a separate call);
+ *   lse (fp32 [batch, num_heads], or NULL): receives each softmax's log2 normaliser in
+ *     the kernel's score units, max_p(s_p) + log2(sum_p exp2(s_p - max)), s_p = scale *
+ *     log2(e) * q . k_p; -inf when no key was live. pkv_merge_attention combines parts.
+ */
+int pkv_paged_decode_ex(void* out, int out_dtype, int64_t out_stride_b, int64_t out_stride_h,
+                        const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                        const void* k_cache, const void* v_cache, int kv_dtype,
+                        int64_t kv_stride_slot, int64_t kv_stride_head, int64_t num_slots,
+                        const int32_t* block_tables, int64_t table_stride, int32_t max_blocks,
+                        const int32_t* context_lens, int32_t batch, int32_t num_heads,
+                        int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                        float scale, int32_t num_workgroups, void* workspace,
+                        int64_t workspace_bytes, const int32_t* first_block, float* lse,
+                        void* stream);
+
+/*
+ * Merge of attentions of the same queries over disjoint key sets: o_tail / lse_tail
+ * (fp32 [batch, num_heads, head_dim] / [batch, num_heads], contiguous) for every
+ * sequence and, for sequence b with prefix_row[b] >= 0, prefix_parts more parts at rows
+ * prefix_row[b] + k * prefix_stride of o_prefix / lse_prefix (same layouts).
+ *   out[b, h] = sum_i w_i o_i / sum_i w_i,  w_i = exp2(lse_i - max_j lse_j),
+ * the softmax over the union of the key sets. Sequences with prefix_row[b] < 0 get
+ * o_tail. No counterpart in the reference.
+ */
+int pkv_merge_attention(void* out, int out_dtype, int64_t out_stride_b, int64_t out_stride_h,
+                        const float* o_tail, const float* lse_tail, const float* o_prefix,
+                        const float* lse_prefix, const int32_t* prefix_row,
+                        int32_t prefix_parts, int64_t prefix_stride, int32_t batch,
+                        int32_t num_heads, int32_t head_dim, void* stream);
+
+/*
  * Chunked-prefill attention over the paged pool, on the matrix cores. Replaces the
  * reference's gather of each chunk's context slots plus FlashAttention varlen call
  * (engine/model/layers.py:246-253, metadata from engine/runtime/paged_cache.py:159-202).
@@ -151,6 +187,26 @@ int pkv_paged_prefill(void* out, int out_dtype, int64_t out_stride_tok, int64_t 
                       const int32_t* context_lens, const int32_t* cu_seqlens_q, int32_t n_chunks,
                       int32_t max_query_len, int32_t num_heads, int32_t num_kv_heads,
                       int32_t head_dim, int32_t block_size, float scale, void* stream);
+
+/*
+ * pkv_paged_prefill with three extras, for the shared-prefix part of cascade decode (no
+ * counterpart in the reference):
+ *   causal = 0: every query of chunk c attends to all n_c keys of its context (the
+ *     shared prefix), instead of the bottom-right causal limit;
+ *   q_rows (int32 [tokens], or NULL = identity): query token t of the step reads q row
+ *     q_rows[t] (a chunk's queries can be rows scattered over the batch); out and lse
+ *     stay in step order;
+ *   lse (fp32 [tokens, num_heads], or NULL): log2 normalisers as in pkv_paged_decode_ex.
+ */
+int pkv_paged_prefill_ex(void* out, int out_dtype, int64_t out_stride_tok, int64_t out_stride_h,
+                         const void* q, int64_t q_stride_tok, int64_t q_stride_h,
+                         const void* k_cache, const void* v_cache, int kv_dtype,
+                         int64_t kv_stride_slot, int64_t kv_stride_head, int64_t num_slots,
+                         const int32_t* block_tables, int64_t table_stride, int32_t max_blocks,
+                         const int32_t* context_lens, const int32_t* cu_seqlens_q,
+                         int32_t n_chunks, int32_t max_query_len, int32_t num_heads,
+                         int32_t num_kv_heads, int32_t head_dim, int32_t block_size, float scale,
+                         int32_t causal, const int32_t* q_rows, float* lse, void* stream);
 
 /*
  * Fused element-wise kernels (csrc/fused.hip). Replace the reference's Triton kernels of

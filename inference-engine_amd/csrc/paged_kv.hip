@@ -356,13 +356,30 @@ struct DecodeArgs {
   float* ws_acc;        // [num_wg, 2, nh, HD] partial records
   float* ws_ml;         // [num_wg, 2, nh, 2]   their (max, sum)
   int out_f32;
+  const int32_t* first_block;  // [batch] or null: attend from table column first_block[b]
+  float* lse;                  // [batch, nh] or null: log2 of each softmax's normaliser
 };
 
-// Clamped context length of sequence b: 0 <= n <= max_blocks * block_size.
+// Table column sequence b starts from (a shared prefix handled elsewhere is skipped).
+__device__ __forceinline__ int first_blk(const DecodeArgs& a, int b) {
+  if (!a.first_block) return 0;
+  const int f = a.first_block[b];
+  return f < 0 ? 0 : (f > a.max_blocks ? a.max_blocks : f);
+}
+
+// Tokens sequence b attends to, clamped: 0 <= n <= (max_blocks - first) * block_size.
+// They are positions first * block_size + p, p < n.
 __device__ __forceinline__ int clamped_ctx(const DecodeArgs& a, int b) {
-  const int n = a.ctx[b];
-  const int cap = a.max_blocks * a.bs;
+  const int fb = first_blk(a, b);
+  const int n = a.ctx[b] - fb * a.bs;
+  const int cap = (a.max_blocks - fb) * a.bs;
   return n < 0 ? 0 : (n > cap ? cap : n);
+}
+
+// Log2 of the softmax normaliser in the kernel's score units (scores x scale x log2 e):
+// max + log2(sum of exp2(score - max)); -inf when no key was live.
+__device__ __forceinline__ float lse_of(float m, float l) {
+  return l > 0.f ? m + __log2f(l) : -INFINITY;
 }
 
 __device__ __forceinline__ int units_of(const DecodeArgs& a, int n) {
@@ -469,10 +486,11 @@ paged_decode_stream_kernel(const DecodeArgs a) {
 
     // Block ids of up to 64 consecutive blocks starting at cb, one per lane.
     int cb = 0, tbl = 0;
+    const int fb = first_blk(a, b);
     auto load_table = [&](int first_block) {
       cb = first_block;
       const int j = cb + lane;
-      tbl = j < a.max_blocks ? a.tables[b * a.table_stride + j] : 0;
+      tbl = j < a.max_blocks - fb ? a.tables[b * a.table_stride + fb + j] : 0;
     };
     auto block_of = [&](int p) { return a.bs_shift >= 0 ? (p >> a.bs_shift) : p / a.bs; };
 
@@ -596,6 +614,7 @@ paged_decode_stream_kernel(const DecodeArgs a) {
           const int64_t e = b * a.out_sb + (int64_t)(h0 + g) * a.out_sh + d0;
           if (a.out_f32) store_vec<PKV_F32, VEC>((float*)a.out + e, o);
           else store_vec<DT, VEC>((S*)a.out + e, o);
+          if (a.lse && lane == 0) a.lse[(int64_t)b * a.nh + h0 + g] = lse_of(m[g], l[g]);
         }
       } else {
 #pragma unroll
@@ -742,10 +761,11 @@ paged_decode_mfma_kernel(const DecodeArgs a) {
     }
 
     int cb = 0, tbl = 0;
+    const int fb = first_blk(a, b);
     auto load_table = [&](int first_block) {
       cb = first_block;
       const int j = cb + lane;
-      tbl = j < a.max_blocks ? a.tables[b * a.table_stride + j] : 0;
+      tbl = j < a.max_blocks - fb ? a.tables[b * a.table_stride + fb + j] : 0;
     };
     auto block_of = [&](int p) { return a.bs_shift >= 0 ? (p >> a.bs_shift) : p / a.bs; };
 
@@ -917,6 +937,7 @@ paged_decode_mfma_kernel(const DecodeArgs a) {
           const int64_t e = b * a.out_sb + (int64_t)(h0 + g) * a.out_sh + d0;
           if (a.out_f32) store_vec<PKV_F32, 8>((float*)a.out + e, o);
           else store_vec<DT, 8>((S*)a.out + e, o);
+          if (a.lse && col == 0) a.lse[(int64_t)b * a.nh + h0 + g] = lse_of(mh[g], lh[g]);
         }
       } else {
 #pragma unroll
@@ -1036,6 +1057,7 @@ paged_decode_combine_kernel(const DecodeArgs a) {
     for (int j0 = 0; j0 < nrec; j0 += kChunk) fold(std::integral_constant<int, kChunk>{}, j0);
   }
   const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+  if (a.lse && lane == 0) a.lse[(int64_t)b * a.nh + h] = lse_of(mmax, lsum);
 #pragma unroll
   for (int k = 0; k < DPL; ++k) {
     const int d = lane + kWave * k;
@@ -1089,6 +1111,9 @@ struct PrefillArgs {
   int32_t pair_halves;  // the whole grid is resident at once: pair heavy with light items
   float scale_log2;
   int out_f32;
+  int32_t causal;         // 0: every query of chunk c sees all its n_c keys
+  const int32_t* q_rows;  // [tokens] or null: query token t reads q row q_rows[t]
+  float* lse;             // [tokens, nh] or null: log2 of each softmax's normaliser
 };
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -1281,14 +1306,15 @@ paged_prefill_kernel(const PrefillArgs a) {
     row_ok[t] = rho < nrows;
     const int rr = row_ok[t] ? rho : 0;
     row_tok[t] = rr / G;
-    const S* qp = reinterpret_cast<const S*>(a.q) + (int64_t)(q0 + row_tok[t]) * a.q_st +
+    const int64_t qrow = a.q_rows ? a.q_rows[q0 + row_tok[t]] : q0 + row_tok[t];
+    const S* qp = reinterpret_cast<const S*>(a.q) + qrow * a.q_st +
                   (int64_t)(kvh * G + rr % G) * a.q_sh + 8 * grp;
 #pragma unroll
     for (int s = 0; s < KS; ++s) qf[t][s] = *reinterpret_cast<const u32x4*>(qp + 32 * s);
   }
   // Keys any row of this workgroup attends to: [0, kend).
   const int last_row = min(nrows - 1, rho0 + BM - 1);
-  const int kend = min(n, base_pos + last_row / G + 1);
+  const int kend = a.causal ? min(n, base_pos + last_row / G + 1) : n;
   const int ntiles = kend > 0 ? (kend + KT - 1) / KT : 0;
 
   // Tile j's K/V rows go from the pool straight into ring stage j % NSTAGE. Instruction
@@ -1370,10 +1396,10 @@ paged_prefill_kernel(const PrefillArgs a) {
 
   // Rows whose causal limit a tile can cross: tile j needs the mask only if it reaches
   // past the smallest limit among this workgroup's rows (its first row's).
-  const int limit_min = min(n - 1, base_pos + rho0 / G);
+  const int limit_min = a.causal ? min(n - 1, base_pos + rho0 / G) : n - 1;
   int limit[RT];  // last key each of this lane's rows sees
 #pragma unroll
-  for (int t = 0; t < RT; ++t) limit[t] = min(n - 1, base_pos + row_tok[t]);
+  for (int t = 0; t < RT; ++t) limit[t] = a.causal ? min(n - 1, base_pos + row_tok[t]) : n - 1;
 
   // Per-lane LDS byte offsets of the operand fragments inside a stage.
   //   K: lane (col, grp) reads key 16 beta + col, chunk 4 s + grp. swz(key) depends on
@@ -1549,6 +1575,9 @@ paged_prefill_kernel(const PrefillArgs a) {
     if (!row_ok[t]) continue;
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     const int rho = rho0 + 16 * RT * wave + 16 * t + col;
+    if (a.lse && grp == 0)  // log2 normaliser: the exponent reference m_run plus log2(sum)
+      a.lse[(int64_t)(q0 + rho / G) * a.nh + kvh * G + rho % G] =
+          l_tot > 0.f ? m_run[t] + __log2f(l_tot) : -INFINITY;
     const int64_t e0 = (int64_t)(q0 + rho / G) * a.out_st + (int64_t)(kvh * G + rho % G) * a.out_sh;
 #pragma unroll
     for (int d = 0; d < DTL; ++d) {
@@ -1562,6 +1591,56 @@ paged_prefill_kernel(const PrefillArgs a) {
                        (uint32_t)Elt<DT>::from_f32(v4[2]) | ((uint32_t)Elt<DT>::from_f32(v4[3]) << 16));
       }
     }
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// Merge of attentions over disjoint key sets (cascade decode: the pieces of a shared
+// prefix and a sequence's private tail). Each part is a normalised output O_i with its
+// log2 normaliser lse_i (kernel score units); the union's softmax is
+//   out = sum_i w_i O_i / sum_i w_i,  w_i = exp2(lse_i - max_j lse_j).
+// Sequence b's prefix parts are rows prefix_row[b] + k * prefix_stride (k < parts) of
+// o_pre / lse_pre; its tail is row b of o_tail / lse_tail. One thread per (sequence,
+// head, dim); a sequence with prefix_row < 0 copies its tail.
+// ---------------------------------------------------------------------------------
+
+template <int DTO>
+__global__ void __launch_bounds__(256)
+merge_attention_kernel(void* __restrict__ out, int64_t osb, int64_t osh,
+                       const float* __restrict__ o_tail, const float* __restrict__ lse_tail,
+                       const float* __restrict__ o_pre, const float* __restrict__ lse_pre,
+                       const int32_t* __restrict__ pre_row, int32_t parts, int64_t pre_stride,
+                       int32_t batch, int32_t nh, int32_t hd) {
+  const int64_t total = (int64_t)batch * nh * hd;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int d = (int)(i % hd);
+    const int64_t bh = i / hd;
+    const int h = (int)(bh % nh);
+    const int b = (int)(bh / nh);
+    float o = o_tail[i];
+    const int r = pre_row[b];
+    if (r >= 0) {
+      const float lt = lse_tail[bh];
+      float m = lt;
+      for (int k = 0; k < parts; ++k) m = fmaxf(m, lse_pre[(r + k * pre_stride) * nh + h]);
+      if (m == -INFINITY) {
+        o = 0.f;
+      } else {
+        float wsum = __builtin_amdgcn_exp2f(lt - m);
+        float acc = wsum * o;
+        for (int k = 0; k < parts; ++k) {
+          const int64_t row = r + k * pre_stride;
+          const float wk = __builtin_amdgcn_exp2f(lse_pre[row * nh + h] - m);  // -inf: 0
+          acc = __builtin_fmaf(wk, o_pre[(row * nh + h) * hd + d], acc);
+          wsum += wk;
+        }
+        o = acc / wsum;
+      }
+    }
+    const int64_t e = (int64_t)b * osb + (int64_t)h * osh + d;
+    if constexpr (DTO == PKV_F32) reinterpret_cast<float*>(out)[e] = o;
+    else reinterpret_cast<typename Elt<DTO>::S*>(out)[e] = Elt<DTO>::from_f32(o);
   }
 }
 
@@ -1907,6 +1986,24 @@ int pkv_paged_decode(void* out, int out_dtype, int64_t out_stride_b, int64_t out
                      int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
                      float scale, int32_t num_workgroups, void* workspace,
                      int64_t workspace_bytes, void* stream) {
+  return pkv_paged_decode_ex(out, out_dtype, out_stride_b, out_stride_h, q, q_stride_b,
+                             q_stride_h, k_cache, v_cache, kv_dtype, kv_stride_slot,
+                             kv_stride_head, num_slots, block_tables, table_stride, max_blocks,
+                             context_lens, batch, num_heads, num_kv_heads, head_dim, block_size,
+                             scale, num_workgroups, workspace, workspace_bytes, nullptr,
+                             nullptr, stream);
+}
+
+int pkv_paged_decode_ex(void* out, int out_dtype, int64_t out_stride_b, int64_t out_stride_h,
+                        const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                        const void* k_cache, const void* v_cache, int kv_dtype,
+                        int64_t kv_stride_slot, int64_t kv_stride_head, int64_t num_slots,
+                        const int32_t* block_tables, int64_t table_stride, int32_t max_blocks,
+                        const int32_t* context_lens, int32_t batch, int32_t num_heads,
+                        int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                        float scale, int32_t num_workgroups, void* workspace,
+                        int64_t workspace_bytes, const int32_t* first_block, float* lse,
+                        void* stream) {
   const int bad = check_decode_shape(kv_dtype, head_dim, num_heads, num_kv_heads);
   if (bad) return bad;
   if (!(out_dtype == kv_dtype || out_dtype == PKV_F32)) return PKV_E_DTYPE;
@@ -1953,6 +2050,8 @@ int pkv_paged_decode(void* out, int out_dtype, int64_t out_stride_b, int64_t out
   a.num_wg = num_workgroups;
   a.scale_log2 = scale * 1.4426950408889634f;
   a.out_f32 = out_dtype == PKV_F32;
+  a.first_block = first_block;
+  a.lse = lse;
   a.desc = nullptr;
   a.ws_acc = nullptr;
   a.ws_ml = nullptr;
@@ -1979,6 +2078,23 @@ int pkv_paged_prefill(void* out, int out_dtype, int64_t out_stride_tok, int64_t 
                       const int32_t* context_lens, const int32_t* cu_seqlens_q, int32_t n_chunks,
                       int32_t max_query_len, int32_t num_heads, int32_t num_kv_heads,
                       int32_t head_dim, int32_t block_size, float scale, void* stream) {
+  return pkv_paged_prefill_ex(out, out_dtype, out_stride_tok, out_stride_h, q, q_stride_tok,
+                              q_stride_h, k_cache, v_cache, kv_dtype, kv_stride_slot,
+                              kv_stride_head, num_slots, block_tables, table_stride, max_blocks,
+                              context_lens, cu_seqlens_q, n_chunks, max_query_len, num_heads,
+                              num_kv_heads, head_dim, block_size, scale, 1, nullptr, nullptr,
+                              stream);
+}
+
+int pkv_paged_prefill_ex(void* out, int out_dtype, int64_t out_stride_tok, int64_t out_stride_h,
+                         const void* q, int64_t q_stride_tok, int64_t q_stride_h,
+                         const void* k_cache, const void* v_cache, int kv_dtype,
+                         int64_t kv_stride_slot, int64_t kv_stride_head, int64_t num_slots,
+                         const int32_t* block_tables, int64_t table_stride, int32_t max_blocks,
+                         const int32_t* context_lens, const int32_t* cu_seqlens_q,
+                         int32_t n_chunks, int32_t max_query_len, int32_t num_heads,
+                         int32_t num_kv_heads, int32_t head_dim, int32_t block_size, float scale,
+                         int32_t causal, const int32_t* q_rows, float* lse, void* stream) {
   if (!(kv_dtype == PKV_BF16 || kv_dtype == PKV_F16)) return PKV_E_DTYPE;
   if (!(out_dtype == kv_dtype || out_dtype == PKV_F32)) return PKV_E_DTYPE;
   if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads || block_size <= 0 ||
@@ -2023,11 +2139,47 @@ int pkv_paged_prefill(void* out, int out_dtype, int64_t out_stride_tok, int64_t 
   a.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz(block_size) : -1;
   a.row_blocks = 0;  // set per head_dim by launch_prefill
   a.pair_halves = 0;
+  a.causal = causal != 0;
+  a.q_rows = q_rows;
+  a.lse = lse;
   a.scale_log2 = scale * 1.4426950408889634f;
   a.out_f32 = out_dtype == PKV_F32;
   hipStream_t st = (hipStream_t)stream;
   return (int)(kv_dtype == PKV_BF16 ? launch_prefill<PKV_BF16>(a, head_dim, rows, st)
                                     : launch_prefill<PKV_F16>(a, head_dim, rows, st));
+}
+
+int pkv_merge_attention(void* out, int out_dtype, int64_t out_stride_b, int64_t out_stride_h,
+                        const float* o_tail, const float* lse_tail, const float* o_prefix,
+                        const float* lse_prefix, const int32_t* prefix_row,
+                        int32_t prefix_parts, int64_t prefix_stride, int32_t batch,
+                        int32_t num_heads, int32_t head_dim, void* stream) {
+  if (!valid_dtype(out_dtype)) return PKV_E_DTYPE;
+  if (batch < 0 || num_heads < 0 || head_dim < 0 || prefix_parts < 0 || prefix_stride < 0)
+    return PKV_E_SHAPE;
+  if (batch == 0 || num_heads == 0 || head_dim == 0) return 0;
+  if (!out || !o_tail || !lse_tail || !o_prefix || !lse_prefix || !prefix_row) return PKV_E_NULL;
+  const int64_t total = (int64_t)batch * num_heads * head_dim;
+  int64_t nb = (total + 255) / 256;
+  if (nb > 8192) nb = 8192;
+  hipStream_t st = (hipStream_t)stream;
+  switch (out_dtype) {
+    case PKV_F32:
+      hipLaunchKernelGGL(merge_attention_kernel<PKV_F32>, dim3((unsigned)nb), dim3(256), 0, st,
+                         out, out_stride_b, out_stride_h, o_tail, lse_tail, o_prefix, lse_prefix,
+                         prefix_row, prefix_parts, prefix_stride, batch, num_heads, head_dim);
+      break;
+    case PKV_F16:
+      hipLaunchKernelGGL(merge_attention_kernel<PKV_F16>, dim3((unsigned)nb), dim3(256), 0, st,
+                         out, out_stride_b, out_stride_h, o_tail, lse_tail, o_prefix, lse_prefix,
+                         prefix_row, prefix_parts, prefix_stride, batch, num_heads, head_dim);
+      break;
+    default:
+      hipLaunchKernelGGL(merge_attention_kernel<PKV_BF16>, dim3((unsigned)nb), dim3(256), 0, st,
+                         out, out_stride_b, out_stride_h, o_tail, lse_tail, o_prefix, lse_prefix,
+                         prefix_row, prefix_parts, prefix_stride, batch, num_heads, head_dim);
+  }
+  return (int)hipGetLastError();
 }
 
 }  // extern "C"

@@ -52,6 +52,30 @@ SIGNATURES: dict[str, tuple] = {
     ),  # fmt: skip
     "pkv_rope": (ctypes.c_int, [_p, ctypes.c_int, _i64, _i64, _p, _p, _i64, _i64, _i32, _i32, _p]),
     "pkv_silu_mul": (ctypes.c_int, [_p, _p, _p, ctypes.c_int, _i64, _p]),
+    "pkv_paged_decode_ex": (
+        ctypes.c_int,
+        [_p, ctypes.c_int, _i64, _i64,            # out
+         _p, _i64, _i64,                          # q
+         _p, _p, ctypes.c_int, _i64, _i64, _i64,  # k, v caches
+         _p, _i64, _i32,                          # block tables
+         _p, _i32, _i32, _i32, _i32, _i32,        # ctx, batch, nh, nkv, hd, bs
+         _f32, _i32, _p, _i64,                    # scale, wgs, workspace
+         _p, _p, _p],                             # first_block, lse, stream
+    ),  # fmt: skip
+    "pkv_paged_prefill_ex": (
+        ctypes.c_int,
+        [_p, ctypes.c_int, _i64, _i64,            # out
+         _p, _i64, _i64,                          # q
+         _p, _p, ctypes.c_int, _i64, _i64, _i64,  # k, v caches
+         _p, _i64, _i32,                          # block tables
+         _p, _p, _i32, _i32,                      # ctx, cu_q, n_chunks, max_query_len
+         _i32, _i32, _i32, _i32, _f32,            # nh, nkv, hd, bs, scale
+         _i32, _p, _p, _p],                       # causal, q_rows, lse, stream
+    ),  # fmt: skip
+    "pkv_merge_attention": (
+        ctypes.c_int,
+        [_p, ctypes.c_int, _i64, _i64, _p, _p, _p, _p, _p, _i32, _i64, _i32, _i32, _i32, _p],
+    ),
     "pkv_paged_prefill": (
         ctypes.c_int,
         [_p, ctypes.c_int, _i64, _i64,            # out

@@ -22,6 +22,9 @@ allocates outside torch's caching allocator or synchronises.
 
 from __future__ import annotations
 
+from collections.abc import Sequence
+from dataclasses import dataclass
+
 import torch
 
 from engine.kernels import _native
@@ -83,6 +86,101 @@ def decode_workspace(device: torch.device, batch: int, num_heads: int, head_dim:
     return torch.empty(nbytes, dtype=torch.uint8, device=device) if nbytes else None
 
 
+@dataclass
+class PrefixGroups:
+    """Decode sequences that share leading KV blocks (a common prompt prefix held once in
+    the pool), laid out for cascade decode. Built by ``find_prefix_groups``; all tensors
+    int32 on the device. With S grouped sequences and K pieces per shared prefix:
+
+    - first_block [B]: blocks of b's shared prefix (0 for ungrouped sequences): the
+      decode pass starts there;
+    - prefix_row [B]: b's row among the grouped sequences (-1: ungrouped); its k-th
+      prefix part is row prefix_row[b] + k * S of the prefix pass;
+    - q_rows [K * S], cu_q [K * C + 1], ctx [K * C], tables [K * C, W']: the prefix pass
+      as K * C non-causal chunks (chunk k * C + g = piece k of group g: the group's
+      queries against blocks [k P_g, (k + 1) P_g) of its prefix).
+    """
+
+    first_block: torch.Tensor
+    prefix_row: torch.Tensor
+    q_rows: torch.Tensor
+    cu_q: torch.Tensor
+    ctx: torch.Tensor
+    tables: torch.Tensor
+    members: int
+    pieces: int
+    max_members: int
+
+
+def find_prefix_groups(block_tables: Sequence[Sequence[int]] | torch.Tensor,
+                       context_lens: Sequence[int] | torch.Tensor, block_size: int,
+                       num_heads: int, num_kv_heads: int, device: torch.device, *,
+                       min_blocks: int = 16,
+                       target_workgroups: int = 512) -> PrefixGroups | None:  # fmt: skip
+    """Group the sequences of a decode batch that start with the same physical blocks.
+
+    Sequences whose first block is the same form a group (at least two members); its
+    shared prefix is the longest run of leading blocks every member's table holds and
+    every member's context covers completely, if it is at least ``min_blocks`` long.
+    Host-side (the tables the engine's block manager produced); returns None when no
+    group qualifies. Each prefix is cut into K pieces so the prefix pass has about
+    ``target_workgroups`` workgroups (K >= 1, pieces of at least 4 blocks)."""
+    tables = torch.as_tensor(block_tables, dtype=torch.int32).cpu()
+    ctx = torch.as_tensor(context_lens, dtype=torch.int64).cpu()
+    b, w = tables.shape
+    full = torch.clamp(ctx // block_size, max=w)
+    groups: list[tuple[torch.Tensor, int]] = []
+    eligible = full >= min_blocks
+    if w and int(eligible.sum()) >= 2:
+        firsts = tables[:, 0].clone()
+        firsts[~eligible] = -1
+        ids, counts = torch.unique(firsts, return_counts=True)
+        for fid, cnt in zip(ids.tolist(), counts.tolist(), strict=True):
+            if fid < 0 or cnt < 2:
+                continue
+            members = torch.nonzero(firsts == fid).flatten()
+            rows = tables[members]
+            lcp = (rows == rows[:1]).int().cumprod(1).sum(1)
+            shared = int(torch.minimum(lcp, full[members]).min())
+            if shared >= min_blocks:
+                groups.append((members, shared))
+    if not groups:
+        return None
+    g_count = len(groups)
+    sizes = [len(m) for m, _ in groups]
+    s_total = sum(sizes)
+    max_members = max(sizes)
+    groups_rows = -(-max_members * (num_heads // num_kv_heads) // 128)
+    per_piece = max(1, groups_rows * num_kv_heads * g_count)
+    min_shared = min(sh for _, sh in groups)
+    pieces = max(1, min(-(-target_workgroups // per_piece), min_shared // 4))
+    first_block = torch.zeros(b, dtype=torch.int32)
+    prefix_row = torch.full((b,), -1, dtype=torch.int32)
+    order = torch.cat([m for m, _ in groups]).to(torch.int32)
+    cu = [0]
+    for (members, shared), size in zip(groups, sizes, strict=True):
+        first_block[members] = shared
+        prefix_row[members] = torch.arange(cu[-1], cu[-1] + size, dtype=torch.int32)
+        cu.append(cu[-1] + size)
+    piece_blocks = [-(-shared // pieces) for _, shared in groups]
+    width = max(max(piece_blocks), 1)
+    ptables = torch.zeros(pieces * g_count, width, dtype=torch.int32)
+    pctx = torch.zeros(pieces * g_count, dtype=torch.int32)
+    cu_q = torch.zeros(pieces * g_count + 1, dtype=torch.int32)
+    for k in range(pieces):
+        for g, ((members, shared), pb) in enumerate(zip(groups, piece_blocks, strict=True)):
+            c = k * g_count + g
+            lo, hi = min(k * pb, shared), min((k + 1) * pb, shared)
+            ptables[c, : hi - lo] = tables[members[0], lo:hi]
+            pctx[c] = (hi - lo) * block_size
+            cu_q[c + 1] = k * s_total + cu[g + 1]
+    dev = torch.device(device)
+    return PrefixGroups(
+        first_block=first_block.to(dev), prefix_row=prefix_row.to(dev),
+        q_rows=order.repeat(pieces).to(dev), cu_q=cu_q.to(dev), ctx=pctx.to(dev),
+        tables=ptables.to(dev), members=s_total, pieces=pieces, max_members=max_members)  # fmt: skip
+
+
 def paged_decode_attention(
     q: torch.Tensor,
     k_cache: torch.Tensor,
@@ -95,6 +193,7 @@ def paged_decode_attention(
     out: torch.Tensor | None = None,
     num_workgroups: int | None = None,
     workspace: torch.Tensor | None = None,
+    prefix_groups: PrefixGroups | None = None,
 ) -> torch.Tensor:
     """q: [B, nh, hd]; k_cache, v_cache: [num_slots, nkv, hd] (one layer);
     block_tables: [B, max_blocks] int32; context_lens: [B] int32 -> [B, nh, hd].
@@ -105,6 +204,11 @@ def paged_decode_attention(
     ``num_workgroups`` overrides how many workgroups share the contexts (default: as many
     as the GPU holds at once); ``workspace`` (uint8, from ``decode_workspace``) replaces
     the scratch otherwise taken from torch's caching allocator on each call.
+    ``prefix_groups`` (from ``find_prefix_groups``) turns on cascade decode for 16-bit
+    caches at head_dim 32-256: each group's shared prefix is read once for all its
+    members on the matrix cores (the chunked-prefill kernel, non-causal), the decode
+    kernel reads only each sequence's private blocks, and a merge kernel combines the two
+    softmaxes by their log-sum-exp. Other shapes ignore it (the plain decode is exact).
     """
     del block_n
     what = "paged_decode_attention"
@@ -148,6 +252,8 @@ def paged_decode_attention(
     if num_workgroups is None:
         num_workgroups = decode_workgroups(dev, q.dtype, hd, nh, nkv)
     lib = _native.lib()
+    cascade = prefix_groups is not None and q.dtype in (torch.bfloat16, torch.float16) \
+        and hd in PREFILL_HEAD_DIMS  # fmt: skip
     ws_bytes = lib.pkv_decode_workspace_bytes(num_workgroups, b, nh, hd)
     ws = None
     if ws_bytes and workspace is not None:
@@ -158,18 +264,58 @@ def paged_decode_attention(
         ws = workspace
     elif ws_bytes:
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-    status = lib.pkv_paged_decode(
-        out.data_ptr(), _native.dtype_code(out.dtype, what), out.stride(0), out.stride(1),
+    dest, lse = out, None
+    if cascade:  # the tail pass writes fp32 parts and their normalisers
+        dest = torch.empty(b, nh, hd, dtype=torch.float32, device=dev)
+        lse = torch.empty(b, nh, dtype=torch.float32, device=dev)
+    status = lib.pkv_paged_decode_ex(
+        dest.data_ptr(), _native.dtype_code(dest.dtype, what), dest.stride(0), dest.stride(1),
         q.data_ptr(), q.stride(0), q.stride(1),
         k_cache.data_ptr(), v_cache.data_ptr(), kv_code,
         k_cache.stride(0), k_cache.stride(1), k_cache.shape[0],
         block_tables.data_ptr(), block_tables.stride(0), max_blocks,
         context_lens.data_ptr(), b, nh, nkv, hd, block_size,
         hd**-0.5, num_workgroups, ws.data_ptr() if ws is not None else None, ws_bytes,
+        prefix_groups.first_block.data_ptr() if cascade else None,
+        lse.data_ptr() if cascade else None, _native.stream_of(dev),
+    )  # fmt: skip
+    _native.check(status, what)
+    if cascade:
+        _cascade_prefix_and_merge(q, k_cache, v_cache, block_size, prefix_groups, dest, lse,
+                                  out)  # fmt: skip
+    return out
+
+
+def _cascade_prefix_and_merge(q, k_cache, v_cache, block_size, pg: PrefixGroups,
+                              o_tail, lse_tail, out) -> None:  # fmt: skip
+    """Prefix pass of cascade decode (every group's queries against its shared blocks,
+    non-causal chunks on the chunked-prefill kernel) and the log-sum-exp merge."""
+    what = "paged_decode_attention (cascade)"
+    b, nh, hd = q.shape
+    nkv = k_cache.shape[1]
+    dev = q.device
+    rows = pg.pieces * pg.members
+    o_pre = torch.empty(rows, nh, hd, dtype=torch.float32, device=dev)
+    lse_pre = torch.empty(rows, nh, dtype=torch.float32, device=dev)
+    kv_code = _native.dtype_code(k_cache.dtype, what)
+    lib = _native.lib()
+    status = lib.pkv_paged_prefill_ex(
+        o_pre.data_ptr(), _native.PKV_F32, o_pre.stride(0), o_pre.stride(1),
+        q.data_ptr(), q.stride(0), q.stride(1),
+        k_cache.data_ptr(), v_cache.data_ptr(), kv_code,
+        k_cache.stride(0), k_cache.stride(1), k_cache.shape[0],
+        pg.tables.data_ptr(), pg.tables.stride(0), pg.tables.shape[1],
+        pg.ctx.data_ptr(), pg.cu_q.data_ptr(), pg.ctx.numel(), pg.max_members,
+        nh, nkv, hd, block_size, hd**-0.5, 0, pg.q_rows.data_ptr(), lse_pre.data_ptr(),
         _native.stream_of(dev),
     )  # fmt: skip
     _native.check(status, what)
-    return out
+    status = lib.pkv_merge_attention(
+        out.data_ptr(), _native.dtype_code(out.dtype, what), out.stride(0), out.stride(1),
+        o_tail.data_ptr(), lse_tail.data_ptr(), o_pre.data_ptr(), lse_pre.data_ptr(),
+        pg.prefix_row.data_ptr(), pg.pieces, pg.members, b, nh, hd, _native.stream_of(dev),
+    )  # fmt: skip
+    _native.check(status, what)
 
 
 def reference_decode_attention(

@@ -1,0 +1,126 @@
+"""Cascade decode over shared prefixes: prefix groups found from the block tables, the
+shared blocks attended once per group (chunked-prefill kernel, non-causal), each
+sequence's private tail by the decode kernel, merged by log-sum-exp. No counterpart in
+the reference (its decode reads every sequence's whole context); the result must be the
+same attention (the reference's semantics, engine/kernels/paged_attention.py:192-211)."""
+
+from __future__ import annotations
+
+import os
+
+import pytest
+import torch
+
+from engine.kernels import paged_attention as pa
+
+THREADS = min(16, os.cpu_count() or 1)
+
+
+def _shared_batch(b=12, shared_blocks=20, bs=16, tails=None, extra=3, seed=0, width=None):
+    """b sequences, the first b - extra holding the same `shared_blocks` blocks first,
+    then private blocks; the last `extra` sequences fully private."""
+    g = torch.Generator().manual_seed(seed)
+    tails = tails if tails is not None else torch.randint(0, 70, (b,), generator=g).tolist()
+    ctx = [shared_blocks * bs + t for t in tails]
+    width = width or max(-(-n // bs) for n in ctx) + 2
+    nblk = shared_blocks + sum(-(-n // bs) for n in ctx) + 5
+    perm = torch.randperm(nblk, generator=g).int()
+    tables = torch.zeros(b, width, dtype=torch.int32)
+    shared = perm[:shared_blocks]
+    at = shared_blocks
+    for i in range(b):
+        nb = -(-ctx[i] // bs)
+        if i < b - extra:
+            tables[i, :shared_blocks] = shared
+            own = nb - shared_blocks
+            tables[i, shared_blocks:nb] = perm[at : at + own]
+            at += own
+        else:
+            tables[i, :nb] = perm[at : at + nb]
+            at += nb
+    return tables, torch.tensor(ctx, dtype=torch.int32), nblk
+
+
+def test_prefix_groups_cover_every_context_exactly():
+    """Per sequence: its prefix pieces (through the piece tables) followed by its tail
+    (through its own table from first_block on) visit exactly its own slots 0 .. n-1."""
+    bs = 16
+    for seed, tails in ((0, None), (1, [0] * 12), (2, [5, 16, 0, 33, 1, 64, 2, 3, 4, 5, 6, 7])):
+        tables, ctx, _ = _shared_batch(tails=tails, seed=seed)
+        pg = pa.find_prefix_groups(tables, ctx, bs, 24, 8, "cpu", min_blocks=4,
+                                   target_workgroups=200)  # fmt: skip
+        assert pg is not None and pg.members == 9
+        s_total = pg.members
+        for b in range(tables.shape[0]):
+            n = int(ctx[b])
+            own = [int(tables[b, p // bs]) * bs + p % bs for p in range(n)]
+            seen = []
+            r = int(pg.prefix_row[b])
+            if r >= 0:
+                for k in range(pg.pieces):
+                    row = r + k * s_total
+                    c = int(torch.searchsorted(pg.cu_q, torch.tensor([row], dtype=torch.int32),
+                                               right=True)) - 1  # fmt: skip
+                    assert int(pg.q_rows[row]) == b
+                    for p in range(int(pg.ctx[c])):
+                        seen.append(int(pg.tables[c, p // bs]) * bs + p % bs)
+            fb = int(pg.first_block[b])
+            assert (r >= 0) == (fb > 0)
+            seen += [int(tables[b, fb + p // bs]) * bs + p % bs for p in range(n - fb * bs)]
+            assert seen == own, b
+
+
+def test_no_groups_when_nothing_is_shared():
+    tables = torch.arange(40, dtype=torch.int32).view(4, 10)
+    assert pa.find_prefix_groups(tables, torch.full((4,), 160), 16, 8, 2, "cpu") is None
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize(("nh", "nkv", "hd", "bs"), [(24, 8, 128, 16), (8, 2, 64, 4), (16, 16, 256, 16)])
+def test_cascade_matches_oracle(dtype, nh, nkv, hd, bs):
+    from oracle import oracle
+
+    dev = torch.device("cuda:0")
+    tails = [0, 1, 15, 16, 17, 40, 100, 3, 0, 9, 60, 2]  # empty tails included
+    tables, ctx, nblk = _shared_batch(tails=tails, bs=bs, seed=hd)
+    g = torch.Generator().manual_seed(7)
+    k = torch.randn(nblk * bs, nkv, hd, generator=g).to(dtype)
+    v = torch.randn(nblk * bs, nkv, hd, generator=g).to(dtype)
+    q = torch.randn(len(tails), nh, hd, generator=g).to(dtype)
+    pg = pa.find_prefix_groups(tables, ctx, bs, nh, nkv, dev, min_blocks=4,
+                               target_workgroups=64)  # fmt: skip
+    assert pg is not None and pg.pieces > 1
+    args = (q.to(dev), k.to(dev), v.to(dev), tables.to(dev), ctx.to(dev), bs)
+    got32 = torch.empty(q.shape, dtype=torch.float32, device=dev)
+    pa.paged_decode_attention(*args, out=got32, prefix_groups=pg)
+    gotq = pa.paged_decode_attention(*args, prefix_groups=pg)
+    torch.cuda.synchronize()
+    want = oracle.decode_attention(q, k, v, tables, ctx, bs, threads=THREADS)
+    assert (got32.cpu() - want).abs().max().item() <= 2e-3
+    assert torch.equal(gotq.cpu(), got32.cpu().to(dtype))
+
+
+@pytest.mark.gpu
+def test_cascade_config3_matches_plain_decode():
+    """Config 3 in full (256 sequences on one 2,048-token prefix, CoW'd last shared
+    block for 64 of them): cascade == the plain decode kernel within 1e-3."""
+    from engine import workloads
+    from engine.runtime.paged_cache import copy_blocks, kv_append
+
+    dev = torch.device("cuda:0")
+    step = workloads.config3(dev, seed=0)
+    copy_blocks(step.k_cache, step.v_cache, step.cow_mapping, step.block_size)
+    kv_append(step.k_cache, step.v_cache, step.new_k, step.new_v, step.slot_mapping)
+    nh, nkv = step.q.shape[1], step.k_cache.shape[1]
+    pg = pa.find_prefix_groups(step.block_tables.cpu(), step.context_lens.cpu(),
+                               step.block_size, nh, nkv, dev)  # fmt: skip
+    assert pg is not None and pg.members == step.batch
+    args = (step.q, step.k_cache, step.v_cache, step.block_tables, step.context_lens,
+            step.block_size)  # fmt: skip
+    plain = torch.empty(step.q.shape, dtype=torch.float32, device=dev)
+    casc = torch.empty_like(plain)
+    pa.paged_decode_attention(*args, out=plain)
+    pa.paged_decode_attention(*args, out=casc, prefix_groups=pg)
+    torch.cuda.synchronize()
+    assert (plain - casc).abs().max().item() <= 1e-3
