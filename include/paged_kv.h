@@ -126,15 +126,31 @@ int pkv_paged_decode(void* out, int out_dtype, int64_t out_stride_b, int64_t out
                      float scale, int32_t num_workgroups, void* workspace,
                      int64_t workspace_bytes, void* stream);
 
+/* Bytes of scratch pkv_paged_decode_ex needs with prefix parts (cascade): the split-K
+ * scratch plus fp32 room for the sequences the stream pass finishes, [batch, num_heads,
+ * head_dim + 1]. Needed at any num_workgroups, 1 included. */
+int64_t pkv_cascade_workspace_bytes(int32_t num_workgroups, int32_t batch, int32_t num_heads,
+                                    int32_t head_dim);
+
 /*
- * pkv_paged_decode with two optional extras, for cascade decode over shared prefixes
- * (no counterpart in the reference, which reads every sequence's whole context):
+ * pkv_paged_decode with optional extras for cascade decode over shared prefixes (no
+ * counterpart in the reference, which reads every sequence's whole context):
  *   first_block (int32 [batch], or NULL = all 0): sequence b attends only to table columns
  *     first_block[b] onwards, i.e. to positions first_block[b] * block_size .. n - 1 (a
  *     shared prefix held in the earlier columns is handled by a separate call);
- *   lse (fp32 [batch, num_heads], or NULL): receives each softmax's log2 normaliser in
- *     the kernel's score units, max_p(s_p) + log2(sum_p exp2(s_p - max)), s_p = scale *
- *     log2(e) * q . k_p; -inf when no key was live. pkv_merge_attention combines parts.
+ *   prefix_out / prefix_lse / prefix_row (fp32 [rows, num_heads, head_dim] contiguous and
+ *     16-byte aligned / fp32 [rows, num_heads] / int32 [batch]; prefix_row NULL or
+ *     prefix_parts 0 = none): attentions of the same queries over other keys, merged
+ *     into the result. For sequence b with prefix_row[b] >= 0, its parts are rows
+ *     prefix_row[b] + k * prefix_stride, k < prefix_parts, each a normalised output O_k
+ *     with log2 normaliser lse_k (pkv_paged_prefill_ex writes both); the result is the
+ *     softmax over the union of the key sets,
+ *       out = (sum_i 2^(lse_i - M) O_i) / (sum_i 2^(lse_i - M)),  M = max_i lse_i,
+ *     over the parts and this call's own keys. The workspace must then hold
+ *     pkv_cascade_workspace_bytes() bytes;
+ *   lse (fp32 [batch, num_heads], or NULL): receives the result's log2 normaliser in the
+ *     kernel's score units, max_p(s_p) + log2(sum_p exp2(s_p - max)), s_p = scale *
+ *     log2(e) * q . k_p, parts included; -inf when no key was live.
  */
 int pkv_paged_decode_ex(void* out, int out_dtype, int64_t out_stride_b, int64_t out_stride_h,
                         const void* q, int64_t q_stride_b, int64_t q_stride_h,
@@ -145,22 +161,9 @@ int pkv_paged_decode_ex(void* out, int out_dtype, int64_t out_stride_b, int64_t 
                         int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
                         float scale, int32_t num_workgroups, void* workspace,
                         int64_t workspace_bytes, const int32_t* first_block, float* lse,
-                        void* stream);
-
-/*
- * Merge of attentions of the same queries over disjoint key sets: o_tail / lse_tail
- * (fp32 [batch, num_heads, head_dim] / [batch, num_heads], contiguous) for every
- * sequence and, for sequence b with prefix_row[b] >= 0, prefix_parts more parts at rows
- * prefix_row[b] + k * prefix_stride of o_prefix / lse_prefix (same layouts).
- *   out[b, h] = sum_i w_i o_i / sum_i w_i,  w_i = exp2(lse_i - max_j lse_j),
- * the softmax over the union of the key sets. Sequences with prefix_row[b] < 0 get
- * o_tail. No counterpart in the reference.
- */
-int pkv_merge_attention(void* out, int out_dtype, int64_t out_stride_b, int64_t out_stride_h,
-                        const float* o_tail, const float* lse_tail, const float* o_prefix,
-                        const float* lse_prefix, const int32_t* prefix_row,
-                        int32_t prefix_parts, int64_t prefix_stride, int32_t batch,
-                        int32_t num_heads, int32_t head_dim, void* stream);
+                        const float* prefix_out, const float* prefix_lse,
+                        const int32_t* prefix_row, int32_t prefix_parts,
+                        int64_t prefix_stride, void* stream);
 
 /*
  * Chunked-prefill attention over the paged pool, on the matrix cores. Replaces the

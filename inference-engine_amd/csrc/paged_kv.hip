@@ -358,6 +358,21 @@ struct DecodeArgs {
   int out_f32;
   const int32_t* first_block;  // [batch] or null: attend from table column first_block[b]
   float* lse;                  // [batch, nh] or null: log2 of each softmax's normaliser
+  // Cascade (pre_row non-null): normalised attentions of the same queries over other
+  // keys (a shared prefix's pieces), merged into the result by the combine pass. Part k
+  // of sequence b is row pre_row[b] + k * pre_stride of pre_o [rows, nh, HD] / pre_lse
+  // [rows, nh] (pre_row[b] < 0: none). The stream pass then writes the sequences it
+  // finishes to out / lse as fp32 scratch, and the combine pass writes every sequence's
+  // result to fin (fin_f32: fp32, else DT) and its normaliser to fin_lse (if non-null).
+  const float* pre_o;
+  const float* pre_lse;
+  const int32_t* pre_row;
+  int32_t pre_parts;
+  int64_t pre_stride;
+  void* fin;
+  int64_t fin_sb, fin_sh;
+  int fin_f32;
+  float* fin_lse;
 };
 
 // Table column sequence b starts from (a shared prefix handled elsewhere is skipped).
@@ -380,6 +395,49 @@ __device__ __forceinline__ int clamped_ctx(const DecodeArgs& a, int b) {
 // max + log2(sum of exp2(score - max)); -inf when no key was live.
 __device__ __forceinline__ float lse_of(float m, float l) {
   return l > 0.f ? m + __log2f(l) : -INFINITY;
+}
+
+// Folds sequence b's prefix parts for head h into a wave's running softmax state (m, l,
+// acc), lane holding head dims lane + 64 c (c < DPL; dims >= HD skipped). A part is a
+// normalised output O_k with log2 normaliser lse_k, i.e. the state (lse_k, 1, O_k):
+// with M the new max, l <- l 2^(m - M) + sum_k 2^(lse_k - M) and likewise acc. Parts
+// are loaded eight at a time, every load issued before any is used.
+template <int HD, int DPL>
+__device__ __forceinline__ void fold_prefix(const DecodeArgs& a, int b, int h, float& m,
+                                            float& l, float (&acc)[DPL]) {
+  const int r = a.pre_row[b];
+  if (r < 0) return;
+  const int lane = threadIdx.x & (kWave - 1);
+  constexpr int C = 8;
+  for (int k0 = 0; k0 < a.pre_parts; k0 += C) {
+    float lk[C], x[C][DPL];
+#pragma unroll
+    for (int jj = 0; jj < C; ++jj) {
+      const int k = k0 + jj;
+      const bool live = k < a.pre_parts;
+      const int64_t row = ((int64_t)r + (int64_t)(live ? k : 0) * a.pre_stride) * a.nh + h;
+      lk[jj] = live ? a.pre_lse[row] : -INFINITY;
+      const float* p = a.pre_o + row * HD;
+#pragma unroll
+      for (int c = 0; c < DPL; ++c) x[jj][c] = lane + kWave * c < HD ? p[lane + kWave * c] : 0.f;
+    }
+    float mn = m;
+#pragma unroll
+    for (int jj = 0; jj < C; ++jj) mn = fmaxf(mn, lk[jj]);
+    const float mref = mn == -INFINITY ? 0.f : mn;  // nothing live yet: weights 0
+    const float alpha = __builtin_amdgcn_exp2f(m - mref);
+    m = mn;
+    l *= alpha;
+#pragma unroll
+    for (int c = 0; c < DPL; ++c) acc[c] *= alpha;
+#pragma unroll
+    for (int jj = 0; jj < C; ++jj) {
+      const float wj = __builtin_amdgcn_exp2f(lk[jj] - mref);  // dead or empty: 0
+      l += wj;
+#pragma unroll
+      for (int c = 0; c < DPL; ++c) acc[c] = __builtin_fmaf(wj, x[jj][c], acc[c]);
+    }
+  }
 }
 
 __device__ __forceinline__ int units_of(const DecodeArgs& a, int n) {
@@ -959,8 +1017,10 @@ paged_decode_mfma_kernel(const DecodeArgs a) {
 // piece, slot 1, unless the range starts with it). One wave per (sequence, query head)
 // merges them: out = sum_j w_j acc_j / sum_j w_j l_j with w_j = exp2(m_j - max m). The
 // sequence's merge plan (16 bytes written by the stream pass) says which records to
-// read; then one round trip per 16 records loads their (m, l) pairs and accumulator
-// rows together. Sequences that were not cut exit after reading the plan.
+// read; then one round trip per 4 records loads their (m, l) pairs and accumulator
+// rows together (4 keeps the kernel near 64 VGPRs, so a whole batch's waves are
+// resident at once). Cascade prefix parts are folded in after the records. Sequences
+// that were not cut exit after reading the plan: the stream pass finished them.
 // ---------------------------------------------------------------------------------
 
 // Total units, and the unit range [ub, ue) of sequence b, in one pass over the lengths.
@@ -993,7 +1053,7 @@ template <int DT, int HD>
 __global__ void __launch_bounds__(256)
 paged_decode_combine_kernel(const DecodeArgs a) {
   constexpr int DPL = HD >= kWave ? HD / kWave : 1;  // head dims per lane
-  constexpr int kChunk = DPL >= 4 ? 16 : 32;          // records loaded per round trip
+  constexpr int kChunk = 4;                           // records loaded per round trip
   const int lane = threadIdx.x & (kWave - 1);
   const int wid = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
   if (wid >= a.batch * a.nh) return;  // uniform per wave
@@ -1001,7 +1061,8 @@ paged_decode_combine_kernel(const DecodeArgs a) {
 
   const int4 plan = a.desc[b];
   const int nrec = plan.y;
-  if (nrec <= 1) return;  // written directly by the stream pass
+  const bool cascade = a.pre_row != nullptr;
+  if (nrec <= 1 && !cascade) return;  // written directly by the stream pass
   const int64_t w0 = plan.x;
   // Units fewer than workgroups leave some ranges empty: then find the live ones.
   int64_t ub = 0, ue = 0, total = 0;
@@ -1015,17 +1076,25 @@ paged_decode_combine_kernel(const DecodeArgs a) {
   // before any is used. Dead slots (past the last record, or an empty range) re-read
   // record 0 -- finite data -- and get weight 0: records that were never written are
   // not read, the scratch may hold NaN bit patterns.
+  // Liveness of records j0 .. j0 + 63, one per lane (a range can be empty only when
+  // units < workgroups; the test divides, so it is done once per lane, not per record).
+  uint64_t live_bits = 0;
+  auto live_block = [&](int j0) {
+    const int j = j0 + lane;
+    bool live = j < nrec;
+    if (!plan.w && live) {
+      const int64_t ww = w0 + j;
+      live = range_start(ww, total, a.num_wg) < range_start(ww + 1, total, a.num_wg);
+    }
+    live_bits = __ballot(live);
+  };
   auto fold = [&](auto chunk, int j0) {
     constexpr int C = decltype(chunk)::value;
     float m[C], l[C], x[C][DPL];
 #pragma unroll
     for (int jj = 0; jj < C; ++jj) {
       const int j = j0 + jj;
-      bool live = j < nrec;
-      if (!plan.w && live) {
-        const int64_t ww = w0 + j;
-        live = range_start(ww, total, a.num_wg) < range_start(ww + 1, total, a.num_wg);
-      }
+      const bool live = (live_bits >> (j & (kWave - 1))) & 1;
       const int64_t row = (live && j > 0) ? (w0 + j) * 2 * a.nh + h : row0;
       const float2 ml = *reinterpret_cast<const float2*>(a.ws_ml + 2 * row);
       m[jj] = live ? ml.x : -INFINITY;
@@ -1051,21 +1120,36 @@ paged_decode_combine_kernel(const DecodeArgs a) {
       for (int k = 0; k < DPL; ++k) out_acc[k] = __builtin_fmaf(wj, x[jj][k], out_acc[k]);
     }
   };
-  if (nrec <= 8) {  // the common case: a sequence cut a few times
-    fold(std::integral_constant<int, 8>{}, 0);
+  if (nrec <= 1) {
+    // Cascade, finished by the stream pass: its normalised fp32 output and log2
+    // normaliser are the state (lse, 1, O); an empty context (-inf) weighs nothing.
+    const float lt = a.lse[(int64_t)b * a.nh + h];
+    mmax = lt;
+    lsum = lt == -INFINITY ? 0.f : 1.f;
+    const float* t = reinterpret_cast<const float*>(a.out) + b * a.out_sb + (int64_t)h * a.out_sh;
+#pragma unroll
+    for (int k = 0; k < DPL; ++k) out_acc[k] = (lane + kWave * k < HD) ? t[lane + kWave * k] : 0.f;
   } else {
-    for (int j0 = 0; j0 < nrec; j0 += kChunk) fold(std::integral_constant<int, kChunk>{}, j0);
+    for (int j0 = 0; j0 < nrec; j0 += kChunk) {
+      if ((j0 & (kWave - 1)) == 0) live_block(j0);
+      fold(std::integral_constant<int, kChunk>{}, j0);
+    }
   }
+  if (cascade) fold_prefix<HD, DPL>(a, b, h, mmax, lsum, out_acc);
   const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-  if (a.lse && lane == 0) a.lse[(int64_t)b * a.nh + h] = lse_of(mmax, lsum);
+  float* lse_dst = cascade ? a.fin_lse : a.lse;
+  if (lse_dst && lane == 0) lse_dst[(int64_t)b * a.nh + h] = lse_of(mmax, lsum);
+  void* dst = cascade ? a.fin : a.out;
+  const int64_t sb = cascade ? a.fin_sb : a.out_sb, sh = cascade ? a.fin_sh : a.out_sh;
+  const bool f32 = cascade ? a.fin_f32 : a.out_f32;
 #pragma unroll
   for (int k = 0; k < DPL; ++k) {
     const int d = lane + kWave * k;
     if (d >= HD) break;
     const float o = out_acc[k] * inv;
-    const int64_t e = b * a.out_sb + (int64_t)h * a.out_sh + d;
-    if (a.out_f32) reinterpret_cast<float*>(a.out)[e] = o;
-    else reinterpret_cast<typename Elt<DT>::S*>(a.out)[e] = Elt<DT>::from_f32(o);
+    const int64_t e = b * sb + (int64_t)h * sh + d;
+    if (f32) reinterpret_cast<float*>(dst)[e] = o;
+    else reinterpret_cast<typename Elt<DT>::S*>(dst)[e] = Elt<DT>::from_f32(o);
   }
 }
 
@@ -1595,60 +1679,42 @@ paged_prefill_kernel(const PrefillArgs a) {
 }
 
 // ---------------------------------------------------------------------------------
-// Merge of attentions over disjoint key sets (cascade decode: the pieces of a shared
-// prefix and a sequence's private tail). Each part is a normalised output O_i with its
-// log2 normaliser lse_i (kernel score units); the union's softmax is
-//   out = sum_i w_i O_i / sum_i w_i,  w_i = exp2(lse_i - max_j lse_j).
-// Sequence b's prefix parts are rows prefix_row[b] + k * prefix_stride (k < parts) of
-// o_pre / lse_pre; its tail is row b of o_tail / lse_tail. One thread per (sequence,
-// head, dim); a sequence with prefix_row < 0 copies its tail.
-// ---------------------------------------------------------------------------------
-
-template <int DTO>
-__global__ void __launch_bounds__(256)
-merge_attention_kernel(void* __restrict__ out, int64_t osb, int64_t osh,
-                       const float* __restrict__ o_tail, const float* __restrict__ lse_tail,
-                       const float* __restrict__ o_pre, const float* __restrict__ lse_pre,
-                       const int32_t* __restrict__ pre_row, int32_t parts, int64_t pre_stride,
-                       int32_t batch, int32_t nh, int32_t hd) {
-  const int64_t total = (int64_t)batch * nh * hd;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const int d = (int)(i % hd);
-    const int64_t bh = i / hd;
-    const int h = (int)(bh % nh);
-    const int b = (int)(bh / nh);
-    float o = o_tail[i];
-    const int r = pre_row[b];
-    if (r >= 0) {
-      const float lt = lse_tail[bh];
-      float m = lt;
-      for (int k = 0; k < parts; ++k) m = fmaxf(m, lse_pre[(r + k * pre_stride) * nh + h]);
-      if (m == -INFINITY) {
-        o = 0.f;
-      } else {
-        float wsum = __builtin_amdgcn_exp2f(lt - m);
-        float acc = wsum * o;
-        for (int k = 0; k < parts; ++k) {
-          const int64_t row = r + k * pre_stride;
-          const float wk = __builtin_amdgcn_exp2f(lse_pre[row * nh + h] - m);  // -inf: 0
-          acc = __builtin_fmaf(wk, o_pre[(row * nh + h) * hd + d], acc);
-          wsum += wk;
-        }
-        o = acc / wsum;
-      }
-    }
-    const int64_t e = (int64_t)b * osb + (int64_t)h * osh + d;
-    if constexpr (DTO == PKV_F32) reinterpret_cast<float*>(out)[e] = o;
-    else reinterpret_cast<typename Elt<DTO>::S*>(out)[e] = Elt<DTO>::from_f32(o);
-  }
-}
-
-// ---------------------------------------------------------------------------------
 // Host-side dispatch.
 // ---------------------------------------------------------------------------------
 
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Decode scratch, byte offsets of its areas (each 256-byte aligned): the merge plans
+// [batch] int4 (split or cascade), the partial records [num_wg, 2, nh, hd] fp32 and
+// their (max, sum) pairs (split: num_wg > 1), and the finished-sequence outputs
+// [batch, nh, hd] fp32 with their normalisers [batch, nh] (cascade). total = 0: no
+// scratch needed.
+struct DecodeWs {
+  int64_t desc = -1, acc = -1, ml = -1, tail_o = -1, tail_lse = -1, total = 0;
+};
+DecodeWs decode_ws(int32_t num_wg, int32_t batch, int32_t nh, int32_t hd, bool cascade) {
+  DecodeWs w;
+  const bool split = num_wg > 1;
+  if (batch <= 0 || nh <= 0 || hd <= 0 || !(split || cascade)) return w;
+  int64_t at = 0;
+  auto place = [&](int64_t bytes) {
+    const int64_t off = (at + 255) / 256 * 256;
+    at = off + bytes;
+    return off;
+  };
+  w.desc = place((int64_t)batch * 16);
+  if (split) {
+    const int64_t recs = (int64_t)num_wg * 2 * nh;
+    w.acc = place(recs * hd * 4);
+    w.ml = place(recs * 2 * 4);
+  }
+  if (cascade) {
+    w.tail_o = place((int64_t)batch * nh * hd * 4);
+    w.tail_lse = place((int64_t)batch * nh * 4);
+  }
+  w.total = at;
+  return w;
+}
 inline int dtype_bytes(int dt) { return dt == PKV_F32 ? 4 : 2; }
 inline bool valid_dtype(int dt) { return dt == PKV_F32 || dt == PKV_F16 || dt == PKV_BF16; }
 
@@ -1758,7 +1824,7 @@ struct LaunchDecode {
       hipLaunchKernelGGL((paged_decode_stream_kernel<DT, HD, GPW>), grid, block, 0, st, *a);
     }
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || a->num_wg <= 1) return e;
+    if (e != hipSuccess || (a->num_wg <= 1 && !a->pre_row)) return e;
     const int waves = a->batch * a->nh;
     hipLaunchKernelGGL((paged_decode_combine_kernel<DT, HD>), dim3((unsigned)((waves + 3) / 4)),
                        dim3(256), 0, st, *a);
@@ -1855,7 +1921,7 @@ hipError_t launch_prefill(const PrefillArgs& a, int hd, int64_t rows, hipStream_
 
 extern "C" {
 
-int pkv_abi_version(void) { return 1; }
+int pkv_abi_version(void) { return 2; }
 
 const char* pkv_status_string(int status) {
   switch (status) {
@@ -1971,10 +2037,12 @@ int32_t pkv_decode_workgroups(int kv_dtype, int32_t head_dim, int32_t num_heads,
 
 int64_t pkv_decode_workspace_bytes(int32_t num_workgroups, int32_t batch, int32_t num_heads,
                                    int32_t head_dim) {
-  if (num_workgroups <= 1 || batch <= 0 || num_heads <= 0 || head_dim <= 0) return 0;
-  const int64_t recs = (int64_t)num_workgroups * 2 * num_heads;
-  return ((int64_t)batch * 16 + 255) / 256 * 256 + (recs * head_dim * 4 + 255) / 256 * 256 +
-         recs * 2 * 4;
+  return decode_ws(num_workgroups, batch, num_heads, head_dim, false).total;
+}
+
+int64_t pkv_cascade_workspace_bytes(int32_t num_workgroups, int32_t batch, int32_t num_heads,
+                                    int32_t head_dim) {
+  return decode_ws(num_workgroups, batch, num_heads, head_dim, true).total;
 }
 
 int pkv_paged_decode(void* out, int out_dtype, int64_t out_stride_b, int64_t out_stride_h,
@@ -1991,7 +2059,7 @@ int pkv_paged_decode(void* out, int out_dtype, int64_t out_stride_b, int64_t out
                              kv_stride_head, num_slots, block_tables, table_stride, max_blocks,
                              context_lens, batch, num_heads, num_kv_heads, head_dim, block_size,
                              scale, num_workgroups, workspace, workspace_bytes, nullptr,
-                             nullptr, stream);
+                             nullptr, nullptr, nullptr, nullptr, 0, 0, stream);
 }
 
 int pkv_paged_decode_ex(void* out, int out_dtype, int64_t out_stride_b, int64_t out_stride_h,
@@ -2003,9 +2071,15 @@ int pkv_paged_decode_ex(void* out, int out_dtype, int64_t out_stride_b, int64_t 
                         int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
                         float scale, int32_t num_workgroups, void* workspace,
                         int64_t workspace_bytes, const int32_t* first_block, float* lse,
-                        void* stream) {
+                        const float* prefix_out, const float* prefix_lse,
+                        const int32_t* prefix_row, int32_t prefix_parts,
+                        int64_t prefix_stride, void* stream) {
   const int bad = check_decode_shape(kv_dtype, head_dim, num_heads, num_kv_heads);
   if (bad) return bad;
+  const bool cascade = prefix_row != nullptr && prefix_parts > 0;
+  if (prefix_parts < 0 || prefix_stride < 0) return PKV_E_SHAPE;
+  if (cascade && (!prefix_out || !prefix_lse)) return PKV_E_NULL;
+  if (cascade && !aligned16(prefix_out)) return PKV_E_ALIGN;
   if (!(out_dtype == kv_dtype || out_dtype == PKV_F32)) return PKV_E_DTYPE;
   if (batch < 0 || block_size <= 0 || max_blocks < 0 || num_workgroups < 1 ||
       num_workgroups > (1 << 24) || batch > (1 << 24))
@@ -2052,18 +2126,39 @@ int pkv_paged_decode_ex(void* out, int out_dtype, int64_t out_stride_b, int64_t 
   a.out_f32 = out_dtype == PKV_F32;
   a.first_block = first_block;
   a.lse = lse;
+  a.pre_o = cascade ? prefix_out : nullptr;
+  a.pre_lse = cascade ? prefix_lse : nullptr;
+  a.pre_row = cascade ? prefix_row : nullptr;
+  a.pre_parts = cascade ? prefix_parts : 0;
+  a.pre_stride = prefix_stride;
+  a.fin = nullptr;
+  a.fin_lse = nullptr;
+  a.fin_sb = a.fin_sh = 0;
+  a.fin_f32 = 0;
   a.desc = nullptr;
   a.ws_acc = nullptr;
   a.ws_ml = nullptr;
-  if (num_workgroups > 1) {
-    const int64_t need = pkv_decode_workspace_bytes(num_workgroups, batch, num_heads, head_dim);
-    if (!workspace || workspace_bytes < need || !aligned16(workspace)) return PKV_E_WORKSPACE;
-    const int64_t recs = (int64_t)num_workgroups * 2 * num_heads;
-    char* p = (char*)workspace;
-    a.desc = (int4*)p;
-    p += ((int64_t)batch * 16 + 255) / 256 * 256;
-    a.ws_acc = (float*)p;
-    a.ws_ml = (float*)(p + (recs * head_dim * 4 + 255) / 256 * 256);
+  const DecodeWs ws = decode_ws(num_workgroups, batch, num_heads, head_dim, cascade);
+  if (ws.total) {
+    if (!workspace || workspace_bytes < ws.total || !aligned16(workspace)) return PKV_E_WORKSPACE;
+    char* base = (char*)workspace;
+    a.desc = (int4*)(base + ws.desc);
+    if (ws.acc >= 0) {
+      a.ws_acc = (float*)(base + ws.acc);
+      a.ws_ml = (float*)(base + ws.ml);
+    }
+    if (cascade) {  // the stream pass finishes sequences into fp32 scratch; combine merges
+      a.fin = out;
+      a.fin_sb = out_stride_b;
+      a.fin_sh = out_stride_h;
+      a.fin_f32 = a.out_f32;
+      a.fin_lse = lse;
+      a.out = base + ws.tail_o;
+      a.out_sb = (int64_t)num_heads * head_dim;
+      a.out_sh = head_dim;
+      a.out_f32 = 1;
+      a.lse = (float*)(base + ws.tail_lse);
+    }
   }
 
   hipStream_t st = (hipStream_t)stream;
@@ -2147,39 +2242,6 @@ int pkv_paged_prefill_ex(void* out, int out_dtype, int64_t out_stride_tok, int64
   hipStream_t st = (hipStream_t)stream;
   return (int)(kv_dtype == PKV_BF16 ? launch_prefill<PKV_BF16>(a, head_dim, rows, st)
                                     : launch_prefill<PKV_F16>(a, head_dim, rows, st));
-}
-
-int pkv_merge_attention(void* out, int out_dtype, int64_t out_stride_b, int64_t out_stride_h,
-                        const float* o_tail, const float* lse_tail, const float* o_prefix,
-                        const float* lse_prefix, const int32_t* prefix_row,
-                        int32_t prefix_parts, int64_t prefix_stride, int32_t batch,
-                        int32_t num_heads, int32_t head_dim, void* stream) {
-  if (!valid_dtype(out_dtype)) return PKV_E_DTYPE;
-  if (batch < 0 || num_heads < 0 || head_dim < 0 || prefix_parts < 0 || prefix_stride < 0)
-    return PKV_E_SHAPE;
-  if (batch == 0 || num_heads == 0 || head_dim == 0) return 0;
-  if (!out || !o_tail || !lse_tail || !o_prefix || !lse_prefix || !prefix_row) return PKV_E_NULL;
-  const int64_t total = (int64_t)batch * num_heads * head_dim;
-  int64_t nb = (total + 255) / 256;
-  if (nb > 8192) nb = 8192;
-  hipStream_t st = (hipStream_t)stream;
-  switch (out_dtype) {
-    case PKV_F32:
-      hipLaunchKernelGGL(merge_attention_kernel<PKV_F32>, dim3((unsigned)nb), dim3(256), 0, st,
-                         out, out_stride_b, out_stride_h, o_tail, lse_tail, o_prefix, lse_prefix,
-                         prefix_row, prefix_parts, prefix_stride, batch, num_heads, head_dim);
-      break;
-    case PKV_F16:
-      hipLaunchKernelGGL(merge_attention_kernel<PKV_F16>, dim3((unsigned)nb), dim3(256), 0, st,
-                         out, out_stride_b, out_stride_h, o_tail, lse_tail, o_prefix, lse_prefix,
-                         prefix_row, prefix_parts, prefix_stride, batch, num_heads, head_dim);
-      break;
-    default:
-      hipLaunchKernelGGL(merge_attention_kernel<PKV_BF16>, dim3((unsigned)nb), dim3(256), 0, st,
-                         out, out_stride_b, out_stride_h, o_tail, lse_tail, o_prefix, lse_prefix,
-                         prefix_row, prefix_parts, prefix_stride, batch, num_heads, head_dim);
-  }
-  return (int)hipGetLastError();
 }
 
 }  // extern "C"

@@ -18,7 +18,7 @@ LIB_PATH = os.path.join(
     "lib",
     "libpaged_kv.so",
 )
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 PKV_F32, PKV_F16, PKV_BF16 = 0, 1, 2
 DTYPE_CODE = {torch.float32: PKV_F32, torch.float16: PKV_F16, torch.bfloat16: PKV_BF16}
@@ -37,6 +37,7 @@ SIGNATURES: dict[str, tuple] = {
     "pkv_decode_slots": (ctypes.c_int, [_p, _p, _i64, _i32, _p, _i32, _i32, _i64, _p]),
     "pkv_decode_workgroups": (_i32, [ctypes.c_int, _i32, _i32, _i32]),
     "pkv_decode_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32]),
+    "pkv_cascade_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32]),
     "pkv_paged_decode": (
         ctypes.c_int,
         [_p, ctypes.c_int, _i64, _i64,            # out
@@ -60,7 +61,9 @@ SIGNATURES: dict[str, tuple] = {
          _p, _i64, _i32,                          # block tables
          _p, _i32, _i32, _i32, _i32, _i32,        # ctx, batch, nh, nkv, hd, bs
          _f32, _i32, _p, _i64,                    # scale, wgs, workspace
-         _p, _p, _p],                             # first_block, lse, stream
+         _p, _p,                                  # first_block, lse
+         _p, _p, _p, _i32, _i64,                  # prefix out, lse, row, parts, stride
+         _p],                                     # stream
     ),  # fmt: skip
     "pkv_paged_prefill_ex": (
         ctypes.c_int,
@@ -72,10 +75,6 @@ SIGNATURES: dict[str, tuple] = {
          _i32, _i32, _i32, _i32, _f32,            # nh, nkv, hd, bs, scale
          _i32, _p, _p, _p],                       # causal, q_rows, lse, stream
     ),  # fmt: skip
-    "pkv_merge_attention": (
-        ctypes.c_int,
-        [_p, ctypes.c_int, _i64, _i64, _p, _p, _p, _p, _p, _i32, _i64, _i32, _i32, _i32, _p],
-    ),
     "pkv_paged_prefill": (
         ctypes.c_int,
         [_p, ctypes.c_int, _i64, _i64,            # out

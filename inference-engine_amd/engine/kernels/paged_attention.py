@@ -78,11 +78,13 @@ def decode_workgroups(device: torch.device, dtype: torch.dtype, head_dim: int,
 
 
 def decode_workspace(device: torch.device, batch: int, num_heads: int, head_dim: int,
-                     num_workgroups: int) -> torch.Tensor | None:  # fmt: skip
+                     num_workgroups: int, *, cascade: bool = False) -> torch.Tensor | None:  # fmt: skip
     """Scratch for ``paged_decode_attention(..., num_workgroups=n, workspace=)``, e.g. to
-    allocate it outside a hipGraph capture (None when the call needs none)."""
-    nbytes = _native.lib().pkv_decode_workspace_bytes(num_workgroups, batch, num_heads,
-                                                      head_dim)  # fmt: skip
+    allocate it outside a hipGraph capture (None when the call needs none); ``cascade``:
+    large enough for a call with ``prefix_groups`` too."""
+    lib = _native.lib()
+    query = lib.pkv_cascade_workspace_bytes if cascade else lib.pkv_decode_workspace_bytes
+    nbytes = query(num_workgroups, batch, num_heads, head_dim)
     return torch.empty(nbytes, dtype=torch.uint8, device=device) if nbytes else None
 
 
@@ -115,16 +117,18 @@ class PrefixGroups:
 def find_prefix_groups(block_tables: Sequence[Sequence[int]] | torch.Tensor,
                        context_lens: Sequence[int] | torch.Tensor, block_size: int,
                        num_heads: int, num_kv_heads: int, device: torch.device, *,
-                       min_blocks: int = 16,
-                       target_workgroups: int = 512) -> PrefixGroups | None:  # fmt: skip
+                       min_blocks: int = 16, target_workgroups: int | None = None,
+                       pieces: int | None = None) -> PrefixGroups | None:  # fmt: skip
     """Group the sequences of a decode batch that start with the same physical blocks.
 
     Sequences whose first block is the same form a group (at least two members); its
     shared prefix is the longest run of leading blocks every member's table holds and
     every member's context covers completely, if it is at least ``min_blocks`` long.
     Host-side (the tables the engine's block manager produced); returns None when no
-    group qualifies. Each prefix is cut into K pieces so the prefix pass has about
-    ``target_workgroups`` workgroups (K >= 1, pieces of at least 4 blocks)."""
+    group qualifies. Each prefix is cut into K pieces (K >= 1, pieces of at least 4
+    blocks), K = ``pieces`` if given, else the most whose prefix pass has at most
+    ``target_workgroups`` workgroups (default: the GPU's CU count, one workgroup per
+    CU -- a second per CU shares the same matrix cores and only adds parts to merge)."""
     tables = torch.as_tensor(block_tables, dtype=torch.int32).cpu()
     ctx = torch.as_tensor(context_lens, dtype=torch.int64).cpu()
     b, w = tables.shape
@@ -153,7 +157,13 @@ def find_prefix_groups(block_tables: Sequence[Sequence[int]] | torch.Tensor,
     groups_rows = -(-max_members * (num_heads // num_kv_heads) // 128)
     per_piece = max(1, groups_rows * num_kv_heads * g_count)
     min_shared = min(sh for _, sh in groups)
-    pieces = max(1, min(-(-target_workgroups // per_piece), min_shared // 4))
+    dev = torch.device(device)
+    if pieces is None:
+        if target_workgroups is None:
+            target_workgroups = torch.cuda.get_device_properties(dev).multi_processor_count \
+                if dev.type == "cuda" else 256  # fmt: skip
+        pieces = target_workgroups // per_piece
+    pieces = max(1, min(pieces, min_shared // 4))
     first_block = torch.zeros(b, dtype=torch.int32)
     prefix_row = torch.full((b,), -1, dtype=torch.int32)
     order = torch.cat([m for m, _ in groups]).to(torch.int32)
@@ -174,7 +184,6 @@ def find_prefix_groups(block_tables: Sequence[Sequence[int]] | torch.Tensor,
             ptables[c, : hi - lo] = tables[members[0], lo:hi]
             pctx[c] = (hi - lo) * block_size
             cu_q[c + 1] = k * s_total + cu[g + 1]
-    dev = torch.device(device)
     return PrefixGroups(
         first_block=first_block.to(dev), prefix_row=prefix_row.to(dev),
         q_rows=order.repeat(pieces).to(dev), cu_q=cu_q.to(dev), ctx=pctx.to(dev),
@@ -206,9 +215,10 @@ def paged_decode_attention(
     the scratch otherwise taken from torch's caching allocator on each call.
     ``prefix_groups`` (from ``find_prefix_groups``) turns on cascade decode for 16-bit
     caches at head_dim 32-256: each group's shared prefix is read once for all its
-    members on the matrix cores (the chunked-prefill kernel, non-causal), the decode
-    kernel reads only each sequence's private blocks, and a merge kernel combines the two
-    softmaxes by their log-sum-exp. Other shapes ignore it (the plain decode is exact).
+    members on the matrix cores (the chunked-prefill kernel, non-causal, one fp32 part
+    per piece with its log-sum-exp), then the decode kernel reads only each sequence's
+    private blocks and merges the parts into its softmax as it finishes each sequence.
+    Other shapes ignore it (the plain decode is exact).
     """
     del block_n
     what = "paged_decode_attention"
@@ -254,7 +264,8 @@ def paged_decode_attention(
     lib = _native.lib()
     cascade = prefix_groups is not None and q.dtype in (torch.bfloat16, torch.float16) \
         and hd in PREFILL_HEAD_DIMS  # fmt: skip
-    ws_bytes = lib.pkv_decode_workspace_bytes(num_workgroups, b, nh, hd)
+    query = lib.pkv_cascade_workspace_bytes if cascade else lib.pkv_decode_workspace_bytes
+    ws_bytes = query(num_workgroups, b, nh, hd)
     ws = None
     if ws_bytes and workspace is not None:
         if workspace.device != dev or workspace.dtype != torch.uint8 or \
@@ -264,45 +275,41 @@ def paged_decode_attention(
         ws = workspace
     elif ws_bytes:
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-    dest, lse = out, None
-    if cascade:  # the tail pass writes fp32 parts and their normalisers
-        dest = torch.empty(b, nh, hd, dtype=torch.float32, device=dev)
-        lse = torch.empty(b, nh, dtype=torch.float32, device=dev)
+    pre = _cascade_prefix(q, k_cache, v_cache, block_size, prefix_groups) if cascade else None
     status = lib.pkv_paged_decode_ex(
-        dest.data_ptr(), _native.dtype_code(dest.dtype, what), dest.stride(0), dest.stride(1),
+        out.data_ptr(), _native.dtype_code(out.dtype, what), out.stride(0), out.stride(1),
         q.data_ptr(), q.stride(0), q.stride(1),
         k_cache.data_ptr(), v_cache.data_ptr(), kv_code,
         k_cache.stride(0), k_cache.stride(1), k_cache.shape[0],
         block_tables.data_ptr(), block_tables.stride(0), max_blocks,
         context_lens.data_ptr(), b, nh, nkv, hd, block_size,
         hd**-0.5, num_workgroups, ws.data_ptr() if ws is not None else None, ws_bytes,
-        prefix_groups.first_block.data_ptr() if cascade else None,
-        lse.data_ptr() if cascade else None, _native.stream_of(dev),
+        prefix_groups.first_block.data_ptr() if cascade else None, None,
+        pre[0].data_ptr() if cascade else None, pre[1].data_ptr() if cascade else None,
+        prefix_groups.prefix_row.data_ptr() if cascade else None,
+        prefix_groups.pieces if cascade else 0, prefix_groups.members if cascade else 0,
+        _native.stream_of(dev),
     )  # fmt: skip
     _native.check(status, what)
-    if cascade:
-        _cascade_prefix_and_merge(q, k_cache, v_cache, block_size, prefix_groups, dest, lse,
-                                  out)  # fmt: skip
     return out
 
 
-def _cascade_prefix_and_merge(q, k_cache, v_cache, block_size, pg: PrefixGroups,
-                              o_tail, lse_tail, out) -> None:  # fmt: skip
-    """Prefix pass of cascade decode (every group's queries against its shared blocks,
-    non-causal chunks on the chunked-prefill kernel) and the log-sum-exp merge."""
+def _cascade_prefix(q, k_cache, v_cache, block_size,
+                    pg: PrefixGroups) -> tuple[torch.Tensor, torch.Tensor]:  # fmt: skip
+    """Prefix pass of cascade decode: every group's queries against its shared blocks,
+    non-causal chunks on the chunked-prefill kernel -> fp32 parts [K * S, nh, hd] and
+    their log2 normalisers [K * S, nh]."""
     what = "paged_decode_attention (cascade)"
-    b, nh, hd = q.shape
+    nh, hd = q.shape[1], q.shape[2]
     nkv = k_cache.shape[1]
     dev = q.device
     rows = pg.pieces * pg.members
     o_pre = torch.empty(rows, nh, hd, dtype=torch.float32, device=dev)
     lse_pre = torch.empty(rows, nh, dtype=torch.float32, device=dev)
-    kv_code = _native.dtype_code(k_cache.dtype, what)
-    lib = _native.lib()
-    status = lib.pkv_paged_prefill_ex(
+    status = _native.lib().pkv_paged_prefill_ex(
         o_pre.data_ptr(), _native.PKV_F32, o_pre.stride(0), o_pre.stride(1),
         q.data_ptr(), q.stride(0), q.stride(1),
-        k_cache.data_ptr(), v_cache.data_ptr(), kv_code,
+        k_cache.data_ptr(), v_cache.data_ptr(), _native.dtype_code(k_cache.dtype, what),
         k_cache.stride(0), k_cache.stride(1), k_cache.shape[0],
         pg.tables.data_ptr(), pg.tables.stride(0), pg.tables.shape[1],
         pg.ctx.data_ptr(), pg.cu_q.data_ptr(), pg.ctx.numel(), pg.max_members,
@@ -310,12 +317,7 @@ def _cascade_prefix_and_merge(q, k_cache, v_cache, block_size, pg: PrefixGroups,
         _native.stream_of(dev),
     )  # fmt: skip
     _native.check(status, what)
-    status = lib.pkv_merge_attention(
-        out.data_ptr(), _native.dtype_code(out.dtype, what), out.stride(0), out.stride(1),
-        o_tail.data_ptr(), lse_tail.data_ptr(), o_pre.data_ptr(), lse_pre.data_ptr(),
-        pg.prefix_row.data_ptr(), pg.pieces, pg.members, b, nh, hd, _native.stream_of(dev),
-    )  # fmt: skip
-    _native.check(status, what)
+    return o_pre, lse_pre
 
 
 def reference_decode_attention(

@@ -50,6 +50,11 @@ def test_workspace_arithmetic():
     recs = 256 * 2 * 24
     assert lib.pkv_decode_workspace_bytes(256, 64, 24, 128) >= 64 * 16 + recs * (128 + 2) * 4
 
+    # cascade: room for every finished sequence's fp32 output and normaliser, any wgs
+    for wgs in (1, 256):
+        plain = lib.pkv_decode_workspace_bytes(wgs, 64, 24, 128)
+        assert lib.pkv_cascade_workspace_bytes(wgs, 64, 24, 128) >= plain + 64 * 24 * 129 * 4
+
     # without a GPU the device query fails cleanly
     if not torch.cuda.is_available():
         assert lib.pkv_decode_workgroups(2, 128, 24, 8) == -6
@@ -76,6 +81,20 @@ def _decode_args(**over):
 def test_decode_rejects_before_launch(over, code):
     """Every rejection happens on the host: these calls never reach the GPU."""
     assert _native.lib().pkv_paged_decode(*_decode_args(**over)) == code
+
+
+@pytest.mark.parametrize(
+    ("pre", "code"),
+    [((None, 1 << 12, 1 << 12, 2, 4), -5), ((1 << 12, None, 1 << 12, 2, 4), -5),
+     (((1 << 12) + 4, 1 << 12, 1 << 12, 2, 4), -3), ((1 << 12, 1 << 12, 1 << 12, -1, 4), -2),
+     ((1 << 12, 1 << 12, 1 << 12, 2, -4), -2)],
+)  # fmt: skip
+def test_cascade_decode_rejects_before_launch(pre, code):
+    """pkv_paged_decode_ex's prefix parts: missing or misaligned buffers and negative
+    counts are refused on the host."""
+    a = _decode_args()
+    args = a[:-1] + [1 << 12, None, *pre, None]  # first_block, lse, prefix..., stream
+    assert _native.lib().pkv_paged_decode_ex(*args) == code
 
 
 def test_append_and_copy_reject_before_launch():

@@ -1,6 +1,6 @@
 """Cascade decode over shared prefixes: prefix groups found from the block tables, the
 shared blocks attended once per group (chunked-prefill kernel, non-causal), each
-sequence's private tail by the decode kernel, merged by log-sum-exp. No counterpart in
+sequence's private tail by the decode kernel, which merges the two by log-sum-exp. No counterpart in
 the reference (its decode reads every sequence's whole context); the result must be the
 same attention (the reference's semantics, engine/kernels/paged_attention.py:192-211)."""
 
@@ -76,9 +76,13 @@ def test_no_groups_when_nothing_is_shared():
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("wgs", [None, 1, 7])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize(("nh", "nkv", "hd", "bs"), [(24, 8, 128, 16), (8, 2, 64, 4), (16, 16, 256, 16)])
-def test_cascade_matches_oracle(dtype, nh, nkv, hd, bs):
+def test_cascade_matches_oracle(dtype, nh, nkv, hd, bs, wgs):
+    """The prefix parts merge where each sequence finishes: in the decode kernel itself
+    for a sequence one workgroup holds whole (every one of them at wgs=1), in the
+    combine pass for one cut between workgroups (many at wgs=7)."""
     from oracle import oracle
 
     dev = torch.device("cuda:0")
@@ -93,8 +97,10 @@ def test_cascade_matches_oracle(dtype, nh, nkv, hd, bs):
     assert pg is not None and pg.pieces > 1
     args = (q.to(dev), k.to(dev), v.to(dev), tables.to(dev), ctx.to(dev), bs)
     got32 = torch.empty(q.shape, dtype=torch.float32, device=dev)
-    pa.paged_decode_attention(*args, out=got32, prefix_groups=pg)
-    gotq = pa.paged_decode_attention(*args, prefix_groups=pg)
+    ws = pa.decode_workspace(dev, len(tails), nh, hd, wgs, cascade=True) if wgs else None
+    pa.paged_decode_attention(*args, out=got32, prefix_groups=pg, num_workgroups=wgs,
+                              workspace=ws)  # fmt: skip
+    gotq = pa.paged_decode_attention(*args, prefix_groups=pg, num_workgroups=wgs)
     torch.cuda.synchronize()
     want = oracle.decode_attention(q, k, v, tables, ctx, bs, threads=THREADS)
     assert (got32.cpu() - want).abs().max().item() <= 2e-3
