@@ -55,6 +55,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-graph", action="store_true", help="time eager calls only")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--only", choices=["cascade"], default=None,
+                    help="time only cascade decode (config c3), e.g. under a profiler")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 5 plain 1 GiB device-to-device copies: the known-size "
                          "kernel that scales rocprofv3's FETCH_SIZE / WRITE_SIZE")  # fmt: skip
@@ -132,7 +134,9 @@ def graph_us(torch, fns, steps: int, warmup: int) -> tuple[float, float]:
     return a.elapsed_time(z) * 1e3 / (reps * len(fns)), wall
 
 
-def bench_decode(args, torch) -> dict:
+def decode_setup(args, torch):
+    """The config's decode step after its copy-on-write and append, the layer pools used
+    in rotation, the output buffer and the workgroup count."""
     from engine import workloads
     from engine.kernels import paged_attention as pa
     from engine.runtime.paged_cache import copy_blocks, kv_append
@@ -147,9 +151,18 @@ def bench_decode(args, torch) -> dict:
         pools.append((torch.randn_like(step.k_cache), torch.randn_like(step.v_cache)))
     b, nh, hd = step.q.shape
     nkv = step.k_cache.shape[1]
-    w = step.block_tables.shape[1]
     wgs = args.workgroups or pa.decode_workgroups(dev, step.q.dtype, hd, nh, nkv)
-    out = torch.empty_like(step.q)
+    return step, pools, torch.empty_like(step.q), wgs
+
+
+def bench_decode(args, torch) -> dict:
+    from engine.kernels import paged_attention as pa
+    from engine.runtime.paged_cache import kv_append
+
+    step, pools, out, wgs = decode_setup(args, torch)
+    b, nh, hd = step.q.shape
+    nkv = step.k_cache.shape[1]
+    w = step.block_tables.shape[1]
 
     def attn_fn(k, v):
         return lambda: pa.paged_decode_attention(
@@ -355,7 +368,18 @@ def main() -> int:
 
     import torch
 
-    line = bench_mixed(args, torch) if args.config == "c5" else bench_decode(args, torch)
+    if args.only == "cascade":
+        if args.config != "c3":
+            print("bench.py: --only cascade needs --config c3 (the shared-prefix batch)",
+                  file=sys.stderr)  # fmt: skip
+            return 2
+        step, pools, out, wgs = decode_setup(args, torch)
+        line = {"config": {"workload": step.name, "layer_pools": len(pools)},
+                **bench_cascade(args, torch, step, pools, out, wgs, step.unique_kv_bytes())}
+    elif args.config == "c5":
+        line = bench_mixed(args, torch)
+    else:
+        line = bench_decode(args, torch)
     if args.copy_calibration:
         src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda:0")
         dst = torch.empty_like(src)
