@@ -32,12 +32,6 @@ constexpr int kWave = 64;
 #ifndef PKV_DECODE_PREFETCH
 #define PKV_DECODE_PREFETCH 1
 #endif
-#ifndef PKV_PREFILL_STAGES
-#define PKV_PREFILL_STAGES 2
-#endif
-#ifndef PKV_PREFILL_WAVES_PER_SIMD
-#define PKV_PREFILL_WAVES_PER_SIMD 2
-#endif
 #ifndef PKV_PREFILL_SETPRIO
 #define PKV_PREFILL_SETPRIO 0
 #endif
@@ -1154,25 +1148,32 @@ paged_decode_combine_kernel(const DecodeArgs a) {
 }
 
 // ---------------------------------------------------------------------------------
-// Chunked-prefill attention on the matrix cores (16-bit K/V, head_dim 64/128/256).
+// Chunked-prefill attention on the matrix cores (16-bit K/V, head_dim 32/64/128/256).
 //
 // Chunk c has q_c query tokens (rows cu_q[c] .. cu_q[c+1] of q) and a context of n_c
 // tokens in the paged pool (its own tokens last): query i sits at position n_c - q_c + i
 // and attends to keys 0 .. n_c - q_c + i (bottom-right causal, as the reference's
 // PagedBatch._mixed / varlen path). For KV head g the query rows are (token, head j of
-// g's group) pairs, rho = token * G + j; a workgroup (4 waves) takes 128 of them, each
-// wave two 16-row tiles, and streams the context in 64-token key tiles:
-//   * K and V tiles are gathered from the pool with 16-byte loads into registers while
-//     the previous tile is being reduced, then stored to LDS with the 16-byte chunks of
-//     each token row XOR-swizzled by the token index (conflict-free operand reads).
+// g's group) pairs, rho = token * G + j. A workgroup of 8 waves takes 128 of them, one
+// work item, and fills a CU:
+//   * Key halves. Waves 0-3 take the item's first half of 64-key tiles, waves 4-7 the
+//     rest; wave w of each half holds rows 32 w .. 32 w + 31 (two 16-row MFMA tiles), and
+//     the two waves of one SIMD (w and w + 4) belong to different halves. At the end the
+//     halves' softmax states (m, l, O) merge through LDS.
+//   * Ping-pong. The halves run one barrier interval apart, alternating a matrix phase
+//     (P.V of the previous tile, QK^T of this one) with a VALU phase (the K/V loads of
+//     later tiles, the softmax of this one), so each SIMD overlaps one wave's MFMAs with
+//     the other's softmax.
+//   * K and V tiles go from the pool straight into LDS (global_load_lds), three
+//     intervals ahead, the 16-byte chunks of each token row XOR-swizzled by the token
+//     index (conflict-free operand reads).
 //   * S^T = K . Q^T with v_mfma_f32_16x16x32 (K rows from LDS as A, Q rows kept in
 //     VGPRs as B): lane (row n, grp g) gets keys 4g + r of each 16-key block for query
-//     row n.
-//   * fp32 online softmax per row (cross-row max/sum with permlane16/32 swaps).
+//     row n. fp32 online softmax per row (cross-row max/sum with permlane16/32 swaps).
 //   * O^T += V^T . P^T: P^T's fragment is the lane's own S^T values (the MFMA's
-//     contraction order over keys is chosen to match), so P needs no lane exchange;
-//     V^T comes from two ds_read_b64_tr_b16 transpose reads per MFMA. The rescale
-//     factor of row n lives in the lanes that hold O^T's row n.
+//     contraction order over keys is chosen to match), so P needs no lane exchange and
+//     takes the registers S had; V^T comes from two ds_read_b64_tr_b16 transpose reads
+//     per MFMA. The rescale factor of row n lives in the lanes that hold O^T's row n.
 // P enters the second product in the K/V type; for bf16 as a hi + lo pair (fp32-like
 // accuracy), for fp16 rounded once.
 // ---------------------------------------------------------------------------------
@@ -1192,7 +1193,6 @@ struct PrefillArgs {
   const int32_t* cu_q;  // [n_chunks + 1] query row offsets
   int32_t n_chunks, nh, nkv, groups, bs, bs_shift;
   int32_t row_blocks;   // 128-row blocks per chunk (static bound)
-  int32_t pair_halves;  // the whole grid is resident at once: pair heavy with light items
   float scale_log2;
   int out_f32;
   int32_t causal;         // 0: every query of chunk c sees all its n_c keys
@@ -1279,6 +1279,11 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 __device__ __forceinline__ void dma16_to_lds(const void* src, uint32_t lds_base) {
   asm volatile("global_load_lds_dwordx4 %0, off" : : "v"(src), "{m0}"(lds_base) : "memory");
 }
+// The same with a wave-uniform 64-bit base in SGPRs and a 32-bit per-lane byte offset.
+__device__ __forceinline__ void dma16_to_lds_s(const void* base, uint32_t off, uint32_t lds_base) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" : : "v"(off), "s"(base), "{m0}"(lds_base)
+               : "memory");
+}
 __device__ __forceinline__ void dma4_to_lds(const void* src, uint32_t lds_base) {
   asm volatile("global_load_lds_dword %0, off" : : "v"(src), "{m0}"(lds_base) : "memory");
 }
@@ -1298,7 +1303,7 @@ __device__ __forceinline__ void mfma_phase_end() {
 
 template <int HD> struct PrefillShape {
   static constexpr int RT = HD >= 256 ? 1 : 2;   // 16-row MFMA tiles per wave
-  static constexpr int BM = 4 * 16 * RT;         // query rows per workgroup (4 waves)
+  static constexpr int BM = 4 * 16 * RT;         // query rows per workgroup (4 waves a half)
   static constexpr int KT = HD >= 256 ? 32 : 64; // keys per tile
   static constexpr int CH = HD / 8;              // 16-byte granules per K/V row
   static constexpr int NBETA = KT / 16;          // 16-key blocks of S^T per tile
@@ -1306,8 +1311,7 @@ template <int HD> struct PrefillShape {
   static constexpr int KS = HD / 32;             // contraction steps over head_dim
   static constexpr int DTL = HD / 16;            // 16-dim tiles of O^T
   static constexpr int NLD = KT * CH / 256;      // granules per thread per tile, K and V each
-  static constexpr int STAGE = 2 * KT * CH;      // granules per ring stage (K, then V)
-  static constexpr int NSTAGE = PKV_PREFILL_STAGES;  // ring depth: NSTAGE-1 tiles load during one
+  static constexpr int TILE = KT * CH;           // granules of one K (or V) tile
   static_assert(NLD >= 1 && KT * CH % 256 == 0, "tile must split evenly over 256 threads");
   static_assert(2 * NLD < 64, "vmcnt range");
   static_assert(KT <= kWave, "a tile's block ids must fit one 64-entry table window");
@@ -1324,37 +1328,31 @@ template <int HD> struct PrefillShape {
   }
 };
 
-template <int V> using ic = std::integral_constant<int, V>;
-
 template <int DT, int HD, bool POW2>
-__global__ void __launch_bounds__(256, PKV_PREFILL_WAVES_PER_SIMD)
+__global__ void __launch_bounds__(512)
 paged_prefill_kernel(const PrefillArgs a) {
   using SH = PrefillShape<HD>;
   constexpr int RT = SH::RT, BM = SH::BM, KT = SH::KT, CH = SH::CH, NBETA = SH::NBETA;
-  constexpr int NSG = SH::NSG, KS = SH::KS, DTL = SH::DTL, NLD = SH::NLD;
-  constexpr int STAGE = SH::STAGE, NSTAGE = SH::NSTAGE;
+  constexpr int NSG = SH::NSG, KS = SH::KS, DTL = SH::DTL, NLD = SH::NLD, TILE = SH::TILE;
   static_assert(HD % 32 == 0 && HD <= 256, "head_dim must be 32..256, a multiple of 32");
   using MMA = Mfma16x16x32Bits<DT>;
   using S = typename Elt<DT>::S;
-  __shared__ __align__(16) u32x4 ring[NSTAGE * STAGE];      // K/V tiles
-  __shared__ __align__(16) int32_t idring[NSTAGE][4][kWave];  // block-table windows, per wave
+  // ring[half][0 = K, 1 = V][stage]: each key half's K and V tiles, two stages each.
+  __shared__ __align__(16) u32x4 ring[2][2][2][TILE];
+  // Block-table windows, per half and wave, in a ring of three (one per tile in flight).
+  __shared__ __align__(16) int32_t idring[2][3][4][kWave];
 
   const int tid = threadIdx.x;
+  const int half = __builtin_amdgcn_readfirstlane(tid >> 8);  // which half of the key tiles
+  const int htid = tid & 255;                                 // thread index inside the half
   const int lane = tid & (kWave - 1);
-  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int wave = __builtin_amdgcn_readfirstlane(htid / kWave);  // rows 32 wave .. (RT = 2)
   const int col = lane & 15, grp = lane >> 4;
   // Work items (chunk, row block, KV head), heaviest first: chunks by context length
   // (longest first), then row blocks from the last (it sees the most keys), KV heads
-  // innermost. A grid larger than the GPU holds runs them in that order, so the longest
-  // items start earliest. When the whole grid is resident at once, workgroups L and
-  // L + N/2 are dealt to the same CU, so the second half takes the items in reverse:
-  // each CU then holds the k-th heaviest and the k-th lightest item.
-  const int nitems = (int)gridDim.x;
-  int item = (int)blockIdx.x;
-  if (a.pair_halves) {
-    const int half = (nitems + 1) / 2;
-    if (item >= half) item = nitems - 1 - (item - half);
-  }
+  // innermost. One workgroup fills a CU, so a grid larger than the GPU runs the items
+  // in this order as CUs free up: the longest start earliest.
+  const int item = (int)blockIdx.x;
   const int kvh = item % a.nkv;
   const int rbi = (item / a.nkv) % a.row_blocks;
   const int crank = item / (a.nkv * a.row_blocks);
@@ -1380,7 +1378,8 @@ paged_prefill_kernel(const PrefillArgs a) {
   const int n = min(max(a.ctx[c], 0), cap);
   const int base_pos = n - qlen;  // position of query token 0
 
-  // This lane's query row in each of its wave's 16-row tiles (B operand column).
+  // This lane's query row in each of its wave's 16-row tiles (B operand column). Both
+  // halves hold the same rows.
   int row_tok[RT];
   bool row_ok[RT];
   u32x4 qf[RT][KS];
@@ -1396,75 +1395,110 @@ paged_prefill_kernel(const PrefillArgs a) {
 #pragma unroll
     for (int s = 0; s < KS; ++s) qf[t][s] = *reinterpret_cast<const u32x4*>(qp + 32 * s);
   }
-  // Keys any row of this workgroup attends to: [0, kend).
+  // Keys any row of this workgroup attends to: [0, kend), in ntiles tiles; half 0 takes
+  // tiles 0 .. ns - 1, half 1 the other ntiles - ns.
   const int last_row = min(nrows - 1, rho0 + BM - 1);
   const int kend = a.causal ? min(n, base_pos + last_row / G + 1) : n;
   const int ntiles = kend > 0 ? (kend + KT - 1) / KT : 0;
+  const int ns = (ntiles + 1) / 2;
+  const int tbeg = half ? ns : 0;
+  const int nt = half ? ntiles - ns : ns;
 
-  // Tile j's K/V rows go from the pool straight into ring stage j % NSTAGE. Instruction
-  // r of wave w fills granules r*256 + 64w .. +63 of a stage, one per lane; granule
-  // (token t, position p) holds chunk p ^ (t % CH) of that token's row, so the MFMA
-  // operand reads below are conflict-free. Positions past the context re-read the last
-  // context token (finite, masked out of the softmax). The 64 block-table entries from
-  // the tile's first block on reach LDS the same way, one tile ahead of the K/V loads
-  // that need them, so the table lookup is never on a tile's critical path.
-  int tok[NLD], chk[NLD];
-#pragma unroll
-  for (int r = 0; r < NLD; ++r) {
-    const int gi = r * 256 + tid;
-    tok[r] = gi / CH;
-    chk[r] = (gi % CH) ^ SH::swz(tok[r]);
-  }
+  // Tile j's K (or V) rows go from the pool straight into LDS. Instruction r of wave w
+  // fills granules r*256 + 64w .. +63 of the tile, one per lane; granule (token t,
+  // position p) holds chunk p ^ swz(t) of that token's row, so the MFMA operand reads
+  // below are conflict-free. Positions past the context re-read the last context token
+  // (finite, masked out of the softmax). The 64 block-table entries from the tile's first
+  // block on reach LDS the same way, two tiles ahead of the K/V loads that need them.
+  // Granule r of this thread: token tok_of(r) of the tile, LDS position chk_of(r).
+  auto tok_of = [&](int r) { return (r * 256 + htid) / CH; };
+  auto chk_of = [&](int r) { return ((r * 256 + htid) % CH) ^ SH::swz(tok_of(r)); };
   const int32_t* trow = a.tables + (int64_t)c * a.table_stride;
   const int nlast = max(n - 1, 0);
   auto blk_of = [&](int p) { return POW2 ? (p >> a.bs_shift) : p / a.bs; };
   const int blast = blk_of(nlast);
-  const uint32_t ring_lds = lds_addr(ring);
-  const uint32_t ids_lds = lds_addr(&idring[0][wave][0]);
-  auto issue_ids = [&](int it) {
-    const int st = it % NSTAGE;
-    const int b = min(blk_of(it * KT) + lane, blast);
-    dma4_to_lds(trow + b, ids_lds + (uint32_t)(st * 4 * kWave * 4));
+  const uint32_t ring_lds = lds_addr(&ring[half][0][0][0]);
+  const uint32_t ids_lds = lds_addr(&idring[half][0][wave][0]);
+  // Local tile m of this half is tile tbeg + m; past the half's end, the last one (the
+  // loads keep their count; their stages are free).
+  auto gtile = [&](int m) { return tbeg + min(m, nt - 1); };
+  auto issue_ids = [&](int m) __attribute__((always_inline)) {
+    const int b = min(blk_of(gtile(m) * KT) + lane, blast);
+    dma4_to_lds(trow + b, ids_lds + (uint32_t)((m % 3) * 4 * kWave * 4));
   };
   // One DMA instruction of one wave covers SEG consecutive keys of a tile. When the block
   // size is a power of two >= SEG those keys share one block: its id is wave-uniform and
   // the address is scalar math plus one per-lane offset.
   constexpr int SEG = kWave / CH;
   const bool seg_uniform = POW2 && a.bs >= SEG;
-  auto issue_kv = [&](int it) {
-    const int st = it % NSTAGE;
-    const int32_t* ids = &idring[st][wave][0];
-    const int b0 = blk_of(it * KT);
-    const uint32_t stage = ring_lds + (uint32_t)(st * STAGE * 16);
+  // Fast path (power-of-two blocks of at least SEG keys, tile inside the context): the
+  // lane's byte offset inside its block is the same for every tile, plus a uniform part
+  // when blocks are longer than a tile.
+  uint32_t lane_off[NLD];
+#pragma unroll
+  for (int r = 0; r < NLD; ++r)
+    lane_off[r] = (uint32_t)(((tok_of(r) & (a.bs - 1)) * a.kv_ss + chk_of(r) * 8) * (int64_t)sizeof(S));
+  const int64_t blk_bytes = (int64_t)a.bs * a.kv_ss * (int64_t)sizeof(S);
+  const int64_t kvh_bytes = (int64_t)kvh * a.kv_sh * (int64_t)sizeof(S);
+  // Per round only a 32 x 32-bit multiply-add in SGPRs: block bytes must fit 32 bits
+  // (they do for any real pool), block ids past the pool read block 0.
+  const bool fast = seg_uniform && blk_bytes <= 0xFFFFFFFFll;
+  const uint32_t blk_bytes32 = (uint32_t)blk_bytes;
+  const uint32_t pool_blocks = (uint32_t)min(a.num_slots / a.bs, (int64_t)0x7FFFFFFF);
+  const char* kv_base[2] = {reinterpret_cast<const char*>(a.k) + kvh_bytes,
+                            reinterpret_cast<const char*>(a.v) + kvh_bytes};
+  // K (kv = 0) or V (kv = 1) of local tile m into stage m % 2.
+  auto issue_tile = [&](int m, int kv) __attribute__((always_inline)) {
+    const int j = gtile(m);
+    const int32_t* ids = &idring[half][m % 3][wave][0];
+    const int b0 = blk_of(j * KT);
+    const char* src = reinterpret_cast<const char*>(kv ? a.v : a.k);
+    const uint32_t dst = ring_lds + (uint32_t)(((kv * 2 + (m & 1)) * TILE) * 16);
     if constexpr (POW2) {
-      if (seg_uniform) {
+      if (fast && (j + 1) * KT <= n) {
+        int id[NLD];
+#pragma unroll
+        for (int r = 0; r < NLD; ++r)  // every id read before the first DMA
+          id[r] = ids[((j * KT + (r * 256 + wave * kWave) / CH) >> a.bs_shift) - b0];
+        const char* base = kv_base[kv] + (uint32_t)(((j * KT) & (a.bs - 1)) * a.kv_ss * (int)sizeof(S));
 #pragma unroll
         for (int r = 0; r < NLD; ++r) {
-          const int seg = it * KT + (r * 256 + wave * kWave) / CH;  // first key, uniform
+          uint32_t bid = (uint32_t)__builtin_amdgcn_readfirstlane(id[r]);
+          bid = bid < pool_blocks ? bid : 0u;  // memory safety only
+          dma16_to_lds_s(base + (uint64_t)bid * blk_bytes32, lane_off[r],
+                         dst + (uint32_t)((r * 256 + wave * kWave) * 16));
+        }
+        return;
+      }
+      if (seg_uniform) {  // the context's last tile: positions past it re-read its last token
+        int id[NLD];
+#pragma unroll
+        for (int r = 0; r < NLD; ++r) {  // every id read before the first DMA
+          const int seg = j * KT + (r * 256 + wave * kWave) / CH;  // first key, uniform
+          id[r] = ids[min(seg >> a.bs_shift, blast) - b0];
+        }
+#pragma unroll
+        for (int r = 0; r < NLD; ++r) {
+          const int seg = j * KT + (r * 256 + wave * kWave) / CH;
           const int blk = min(seg >> a.bs_shift, blast);
-          int64_t id = __builtin_amdgcn_readfirstlane(ids[blk - b0]);
-          if (id < 0 || (id + 1) * a.bs > a.num_slots) id = 0;  // memory safety only
-          const int64_t base = (id * a.bs * a.kv_ss + (int64_t)kvh * a.kv_sh) * (int64_t)sizeof(S);
+          int64_t bid = __builtin_amdgcn_readfirstlane(id[r]);
+          if (bid < 0 || (bid + 1) * a.bs > a.num_slots) bid = 0;  // memory safety only
+          const int64_t base = (bid * a.bs * a.kv_ss + (int64_t)kvh * a.kv_sh) * (int64_t)sizeof(S);
           const int in_blk = min(seg + lane / CH, nlast) - blk * a.bs;
-          const uint32_t lo = (uint32_t)((in_blk * a.kv_ss + chk[r] * 8) * (int64_t)sizeof(S));
-          const uint32_t dk = stage + (uint32_t)((r * 256 + wave * kWave) * 16);
-          dma16_to_lds(reinterpret_cast<const char*>(a.k) + base + lo, dk);
-          dma16_to_lds(reinterpret_cast<const char*>(a.v) + base + lo,
-                       dk + (uint32_t)(KT * CH * 16));
+          const uint32_t lo = (uint32_t)((in_blk * a.kv_ss + chk_of(r) * 8) * (int64_t)sizeof(S));
+          dma16_to_lds(src + base + lo, dst + (uint32_t)((r * 256 + wave * kWave) * 16));
         }
         return;
       }
     }
 #pragma unroll
     for (int r = 0; r < NLD; ++r) {
-      const int p = min(it * KT + tok[r], nlast);
+      const int p = min(j * KT + tok_of(r), nlast);
       const int blk = blk_of(p);
       int64_t sl = (int64_t)ids[blk - b0] * a.bs + (p - blk * a.bs);
       sl = (sl >= 0 && sl < a.num_slots) ? sl : 0;
-      const int64_t off = sl * a.kv_ss + (int64_t)kvh * a.kv_sh + chk[r] * 8;
-      const uint32_t dk = stage + (uint32_t)((r * 256 + wave * kWave) * 16);
-      dma16_to_lds(reinterpret_cast<const S*>(a.k) + off, dk);
-      dma16_to_lds(reinterpret_cast<const S*>(a.v) + off, dk + (uint32_t)(KT * CH * 16));
+      const int64_t off = (sl * a.kv_ss + (int64_t)kvh * a.kv_sh + chk_of(r) * 8) * (int64_t)sizeof(S);
+      dma16_to_lds(src + off, dst + (uint32_t)((r * 256 + wave * kWave) * 16));
     }
   };
 
@@ -1481,109 +1515,134 @@ paged_prefill_kernel(const PrefillArgs a) {
   // Rows whose causal limit a tile can cross: tile j needs the mask only if it reaches
   // past the smallest limit among this workgroup's rows (its first row's).
   const int limit_min = a.causal ? min(n - 1, base_pos + rho0 / G) : n - 1;
+  const int j_mask = min(ntiles, max(0, (limit_min + 1) / KT));
   int limit[RT];  // last key each of this lane's rows sees
 #pragma unroll
   for (int t = 0; t < RT; ++t) limit[t] = a.causal ? min(n - 1, base_pos + row_tok[t]) : n - 1;
 
-  // Per-lane LDS byte offsets of the operand fragments inside a stage.
+  // Per-lane LDS byte offsets of the operand fragments inside a tile, recomputed where
+  // they are used (a few VALU instructions; holding them would cost 12 registers).
   //   K: lane (col, grp) reads key 16 beta + col, chunk 4 s + grp. swz(key) depends on
   //      beta only when a row has more than 16 chunks (head_dim 256).
   //   V^T: lane (col, grp) reads key 32 sg + 16 h2 + 4 grp + col / 4, dims 16 d +
   //      4 (col % 4) .. +4 (chunk 2 d + (col % 4) / 2, half (col % 4) & 1).
   constexpr int KSW = CH > 16 ? NBETA : 1;
   constexpr int VSW = CH > 16 ? 2 : 1;
-  uint32_t koff[KSW][KS], voff[VSW][DTL];
-#pragma unroll
-  for (int b = 0; b < KSW; ++b)
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      const int tk = 16 * b + col;
-      koff[b][s] = (uint32_t)(((4 * s + grp) ^ SH::swz(tk)) * 16 + col * CH * 16);
-    }
-#pragma unroll
-  for (int h2 = 0; h2 < VSW; ++h2)
-#pragma unroll
-    for (int d = 0; d < DTL; ++d) {
-      const int tk = 16 * h2 + 4 * grp + col / 4;
-      const int chunk = 2 * d + (col % 4) / 2;
-      voff[h2][d] = (uint32_t)(((chunk ^ SH::swz(tk)) * 16 + (col % 4 & 1) * 8) +
-                               (4 * grp + col / 4) * CH * 16);
-    }
+  auto fresh_lane = [&]() {  // lane, as a value the compiler must not hoist
+    int l = lane;
+    __asm__ volatile("" : "+v"(l));
+    return l;
+  };
+  auto koff = [&](int l, int b, int s) {
+    const int tk = 16 * b + (l & 15);
+    return (uint32_t)(((4 * s + (l >> 4)) ^ SH::swz(tk)) * 16 + (l & 15) * CH * 16);
+  };
+  auto voff = [&](int l, int h2, int d) {
+    const int c4 = l & 3, tr = 4 * (l >> 4) + ((l & 15) >> 2);
+    const int tk = 16 * h2 + tr;
+    return (uint32_t)((((2 * d + c4 / 2) ^ SH::swz(tk)) * 16 + (c4 & 1) * 8) + tr * CH * 16);
+  };
 
-  // One tile of work on ring stage j % NSTAGE; MASK: some key of the tile is past some row's
-  // causal limit (only the tiles on the diagonal and at the context end).
-  auto compute = [&](int j, auto MASK) {
-    constexpr bool masked = decltype(MASK)::value != 0;
-    const int kt0 = j * KT;
-    const char* stage = reinterpret_cast<const char*>(ring) + (j % NSTAGE) * STAGE * 16;
-    // Operand fragments come from LDS at a per-lane offset (koff / voff) plus a
-    // compile-time constant: K by 16-byte reads, V^T by ds_read_b64_tr_b16 transpose
-    // reads.
-    auto kfrag = [&](int beta, int s) {
-      return *reinterpret_cast<const u32x4*>(stage + beta * 16 * CH * 16 +
-                                             koff[KSW == 1 ? 0 : beta][s]);
-    };
-    const char* vstage = stage + KT * CH * 16;
-    auto vfrag = [&](int sg, int d) {
-      u32x4 v;
-#pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2) {
-        // generic -> LDS address space (an addrspacecast of a __shared__ pointer)
-        const s16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_s16x4*)(vstage + (32 * sg + 16 * h2) * CH * 16 + voff[VSW == 1 ? 0 : h2][d]));
-        const uint32_t lo = (uint32_t)(uint16_t)x[0] | ((uint32_t)(uint16_t)x[1] << 16);
-        const uint32_t hi = (uint32_t)(uint16_t)x[2] | ((uint32_t)(uint16_t)x[3] << 16);
-        if (h2 == 0) { v.x = lo; v.y = hi; } else { v.z = lo; v.w = hi; }
-      }
-      return v;
-    };
+  // S^T of a tile from its QK^T to its softmax, then in the same registers its P^T
+  // fragments until its P.V: 32-key step sg's hi and lo parts replace score blocks 2 sg
+  // and 2 sg + 1 (8 scores -> 8 operand words).
+  static_assert(NBETA == 2 * NSG, "two score blocks per P^T fragment pair");
+  f32x4 sc[RT][NBETA];
 
-    // S^T = K . Q^T: block beta holds keys 16 beta + 4 grp + r for query row col.
-    f32x4 sc[RT][NBETA];
-    mfma_phase_begin();
+  // S^T = K . Q^T of local tile m: block beta holds keys 16 beta + 4 grp + r for query
+  // row col.
+  auto qk = [&](int m) __attribute__((always_inline)) {
+    const char* stage = reinterpret_cast<const char*>(&ring[half][0][m & 1][0]);
+    const int l = fresh_lane();
 #pragma unroll
     for (int beta = 0; beta < NBETA; ++beta) {
+      if (beta) __builtin_amdgcn_sched_barrier(0);  // one 16-key block's K fragments at a time
 #pragma unroll
       for (int t = 0; t < RT; ++t) sc[t][beta] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        const u32x4 kf = kfrag(beta, s);
+        const u32x4 kf = *reinterpret_cast<const u32x4*>(stage + beta * 16 * CH * 16 +
+                                                         koff(l, KSW == 1 ? 0 : beta, s));
 #pragma unroll
         for (int t = 0; t < RT; ++t) sc[t][beta] = MMA::mma(kf, qf[t][s], sc[t][beta]);
       }
     }
-    mfma_phase_end();
-
-
-    u32x4 pb[RT][NSG], pl[RT][NSG];  // P^T fragments (hi, lo)
+  };
+  // O^T += V^T . P^T of local tile m; each V^T fragment (two ds_read_b64_tr_b16
+  // transpose reads) serves every row tile.
+  auto pv = [&](int m) __attribute__((always_inline)) {
+    const char* vstage = reinterpret_cast<const char*>(&ring[half][1][m & 1][0]);
+    const int l = fresh_lane();
+#pragma unroll
+    for (int sg = 0; sg < NSG; ++sg) {
+      if (sg) __builtin_amdgcn_sched_barrier(0);  // one 32-key step's fragments at a time
+#pragma unroll
+      for (int d = 0; d < DTL; ++d) {
+        u32x4 vf;
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+          // generic -> LDS address space (an addrspacecast of a __shared__ pointer)
+          const s16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_s16x4*)(vstage + (32 * sg + 16 * h2) * CH * 16 + voff(l, VSW == 1 ? 0 : h2, d)));
+          const uint32_t lo = (uint32_t)(uint16_t)x[0] | ((uint32_t)(uint16_t)x[1] << 16);
+          const uint32_t hi = (uint32_t)(uint16_t)x[2] | ((uint32_t)(uint16_t)x[3] << 16);
+          if (h2 == 0) { vf.x = lo; vf.y = hi; } else { vf.z = lo; vf.w = hi; }
+        }
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+          o[t][d] = MMA::mma(vf, __builtin_bit_cast(u32x4, sc[t][2 * sg]), o[t][d]);
+          if constexpr (MMA::kSplit)
+            o[t][d] = MMA::mma(vf, __builtin_bit_cast(u32x4, sc[t][2 * sg + 1]), o[t][d]);
+        }
+      }
+    }
+  };
+  // Online softmax of global tile j's scores into P^T fragments; masked: some key of the
+  // tile is past some row's causal limit (the tiles on the diagonal and the context end;
+  // a wave-uniform branch around the mask only: one copy of the rest, whose registers a
+  // second copy would double).
+  auto softmax = [&](int j, bool masked) __attribute__((always_inline)) {
+    const int kt0 = j * KT;
+    // p = exp2(scale_log2 * s - m_run). The reference m_run is raised only when a score
+    // exceeds it by more than 2^8: a stale reference changes nothing in O / l (both carry
+    // the same factor), keeps p <= 256, and leaves O untouched on most tiles. The row
+    // tiles are independent chains: maxima first, one rescale branch, then every exp.
+    float mx[RT];
+    bool raise[RT];
+    bool any = false;
 #pragma unroll
     for (int t = 0; t < RT; ++t) {
-      // Online softmax of row col in the log2 domain, p = exp2(scale_log2 * s - m_run).
-      // The reference m_run is raised only when a score exceeds it by more than 2^8:
-      // a stale reference changes nothing in O / l (both carry the same factor), keeps
-      // p <= 256, and leaves O untouched on most tiles.
-      if constexpr (masked) {
+      if (masked) {
+        const int lim = limit[t] - kt0 - 4 * grp;  // keys 16 beta + r past it are out
 #pragma unroll
         for (int beta = 0; beta < NBETA; ++beta)
 #pragma unroll
           for (int r = 0; r < 4; ++r)
-            if (kt0 + 16 * beta + 4 * grp + r > limit[t]) sc[t][beta][r] = -INFINITY;
+            if (16 * beta + r > lim) sc[t][beta][r] = -INFINITY;
       }
-      float mx = -INFINITY;
+      float x = -INFINITY;
 #pragma unroll
       for (int beta = 0; beta < NBETA; ++beta)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sc[t][beta][r]);
-      mx = rows_max(mx) * a.scale_log2;
-      const bool raise = mx > m_run[t] + 8.f;  // also true the first time (m_run = -inf)
-      if (__builtin_amdgcn_ballot_w64(raise)) {  // wave-uniform
-        const float mn = raise ? mx : m_run[t];
-        const float alpha = __builtin_amdgcn_exp2f(m_run[t] - mn);  // 0 when m_run = -inf
-        m_run[t] = mn;
+        for (int r = 0; r < 4; ++r) x = fmaxf(x, sc[t][beta][r]);
+      mx[t] = rows_max(x) * a.scale_log2;
+      raise[t] = mx[t] > m_run[t] + 8.f;  // also true the first time (m_run = -inf)
+      any = any || raise[t];
+    }
+    if (__builtin_amdgcn_ballot_w64(any)) {  // wave-uniform
+#pragma unroll
+      for (int t = 0; t < RT; ++t) {
+        // Rows that do not raise keep their factor 1 (their m_run may still be -inf: a
+        // half's tiles can all lie past a row's causal limit).
+        const float alpha = raise[t] ? __builtin_amdgcn_exp2f(m_run[t] - mx[t]) : 1.f;
+        m_run[t] = raise[t] ? mx[t] : m_run[t];
         l_run[t] *= alpha;
 #pragma unroll
         for (int d = 0; d < DTL; ++d) o[t][d] *= alpha;
       }
+    }
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
       const float mref = m_run[t] == -INFINITY ? 0.f : m_run[t];
       float psum = 0.f;
 #pragma unroll
@@ -1597,59 +1656,114 @@ paged_prefill_kernel(const PrefillArgs a) {
         }
         // P^T fragment: the lane's own 8 probabilities (keys 32 sg + 16 (e / 4) + 4 grp
         // + e % 4), matching the transpose-read order of V^T.
-        MMA::pack8(p, pb[t][sg], pl[t][sg]);
+        u32x4 hi, lo;
+        MMA::pack8(p, hi, lo);
+        sc[t][2 * sg] = __builtin_bit_cast(f32x4, hi);
+        sc[t][2 * sg + 1] = __builtin_bit_cast(f32x4, lo);
       }
       l_run[t] += psum;
     }
-
-    // O^T += V^T . P^T; each V^T fragment serves every row tile.
-    mfma_phase_begin();
-#pragma unroll
-    for (int sg = 0; sg < NSG; ++sg)
-#pragma unroll
-      for (int d = 0; d < DTL; ++d) {
-        const u32x4 vf = vfrag(sg, d);
-#pragma unroll
-        for (int t = 0; t < RT; ++t) {
-          o[t][d] = MMA::mma(vf, pb[t][sg], o[t][d]);
-          if constexpr (MMA::kSplit) o[t][d] = MMA::mma(vf, pl[t][sg], o[t][d]);
-        }
-      }
-    mfma_phase_end();
   };
 
-  // Pipeline, prefetch distance D = NSTAGE - 1. Issue order (per wave):
-  //   ids(0) .. ids(D), [wait all], KV(0) .. KV(D-1), then per tile j:
-  //   wait until KV(j) and ids(j+D) have landed; barrier (every wave's share of KV(j)
-  //   landed, and every wave is done with the stages ids(j+D+1) and KV(j+D) reuse);
-  //   ids(j+D+1); KV(j+D); compute(j).
-  // At the wait the only loads issued after ids(j+D) are the K/V tiles j+1 .. j+D-1 that
-  // exist (2 NLD loads each): waiting down to that many outstanding completes KV(j) and
-  // ids(j+D) (loads complete in issue order). Block ids are always fetched (clamped to
-  // the context's last block), so the counts do not change near the end.
-  constexpr int D = NSTAGE - 1;
-  static_assert(D == 1 || D == 2, "ring of 2 or 3 stages");
-  if (ntiles > 0) {
-#pragma unroll
-    for (int k = 0; k <= D; ++k) issue_ids(k);
+  // Ping-pong schedule. Interval k (k = 0 .. 2 ns + 1) starts at a workgroup barrier; a
+  // half is at local phase p = k - half, so when one half issues matrix work the other
+  // does its softmax, and each SIMD (one wave of each half) overlaps the two.
+  //   p = 2m (matrix phase):  P.V of tile m - 1, QK^T of tile m.
+  //   p = 2m + 1 (VALU phase): loads of block ids (tile m + 3), V (m + 1), K (m + 2);
+  //                            softmax of tile m.
+  // A K tile is used at phase 2m, its V at 2m + 2; both were issued at 2m - 3, into the
+  // stage that tile m - 2 freed at 2m - 2. Before each matrix phase a wave waits for all
+  // but the loads of the previous VALU phase (2 NLD + 1), before each VALU phase for
+  // all but that phase's K and V loads (its block ids must be in). Loads complete in
+  // issue order.
+  if (nt > 0) {  // prologue: block ids of tiles 0-2, K of 0 and 1, V of 0
+    issue_ids(0);
+    issue_ids(1);
     wait_vmcnt<0>();
+    issue_tile(0, 0);
+    issue_ids(2);
+    issue_tile(0, 1);
+    issue_tile(1, 0);
+    wait_vmcnt<0>();
+  }
+  // Matrix phase of iteration m and VALU phase of iteration m, each closed by its
+  // barrier. Half 0 runs intervals (M0 V0)(M1 V1)..(M_ns V_ns); half 1 one interval
+  // later: idle, (M0 V0)..(M_ns-1 V_ns-1) M_ns. Both pass 2 ns + 2 barriers.
+  auto interval_m = [&](int m) __attribute__((always_inline)) {
+    if (m >= 1 && m - 1 < nt) wait_vmcnt<2 * NLD + 1>();
+    else wait_vmcnt<0>();
+    wait_lgkm0();
+    __builtin_amdgcn_s_barrier();
+    mfma_phase_begin();
+    if (m >= 1 && m - 1 < nt) pv(m - 1);  // first: P's registers then hold S
+    // Nothing crosses: the V^T and K fragments of the two products are never all live.
+    __builtin_amdgcn_sched_barrier(0);
+    if (m < nt) qk(m);
+    mfma_phase_end();
+  };
+  auto interval_v = [&](int m) __attribute__((always_inline)) {
+    if (m < nt) wait_vmcnt<2 * NLD>();
+    wait_lgkm0();
+    __builtin_amdgcn_s_barrier();
+    if (m >= nt) return;
+    issue_ids(m + 3);
+    issue_tile(m + 1, 1);
+    issue_tile(m + 2, 0);
+    softmax(tbeg + m, tbeg + m >= j_mask);
+  };
+  if (half == 0) {
+    for (int m = 0; m <= ns; ++m) {
+      interval_m(m);
+      interval_v(m);
+    }
+  } else {
+    wait_lgkm0();
+    __builtin_amdgcn_s_barrier();
+    for (int m = 0; m < ns; ++m) {
+      interval_m(m);
+      interval_v(m);
+    }
+    interval_m(ns);
+  }
+
+  // Merge the halves' softmax states through LDS (the rings are free now): half 1
+  // writes (m, l, O) per lane, half 0 reads its partner lane's (same rows, same lane
+  // layout) and scales both by 2^(m_half - max).
+  constexpr int NE = RT * (2 + 4 * DTL);  // floats per lane
+  static_assert(4 * NE * kWave * 4 <= (int)sizeof(ring), "merge exchange must fit the rings");
+  float* xch = reinterpret_cast<float*>(&ring[0][0][0][0]) + wave * NE * kWave + lane;
+  // The last VALU phases issued loads nothing waited for (past the half's end, into
+  // free stages); they must land before the rings are reused.
+  wait_vmcnt<0>();
+  __syncthreads();
+  if (half) {
 #pragma unroll
-    for (int k = 0; k < D; ++k)
-      if (k < ntiles) issue_kv(k);
-    auto step = [&](int j, auto MASK) {
-      if (D == 2 && j + 1 < ntiles) wait_vmcnt<2 * NLD>();
-      else wait_vmcnt<0>();
-      wait_lgkm0();
-      __builtin_amdgcn_s_barrier();
-      issue_ids(j + D + 1);
-      if (j + D < ntiles) issue_kv(j + D);
-      compute(j, MASK);
-    };
-    // Tile j needs the causal mask iff j * KT + KT - 1 > limit_min: the tiles from
-    // j_mask on. Two loops, so each holds one variant of the tile code.
-    const int j_mask = min(ntiles, max(0, (limit_min + 1) / KT));
-    for (int j = 0; j < j_mask; ++j) step(j, ic<0>{});
-    for (int j = j_mask; j < ntiles; ++j) step(j, ic<1>{});
+    for (int t = 0; t < RT; ++t) {
+      float* x = xch + t * (2 + 4 * DTL) * kWave;
+      x[0] = m_run[t];
+      x[kWave] = l_run[t];
+#pragma unroll
+      for (int d = 0; d < DTL; ++d)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) x[(2 + 4 * d + r) * kWave] = o[t][d][r];
+    }
+  }
+  __syncthreads();
+  if (half) return;
+#pragma unroll
+  for (int t = 0; t < RT; ++t) {
+    const float* x = xch + t * (2 + 4 * DTL) * kWave;
+    const float mb = x[0];
+    const float mn = fmaxf(m_run[t], mb);
+    const float mref = mn == -INFINITY ? 0.f : mn;  // both empty: weights 0
+    const float sa = __builtin_amdgcn_exp2f(m_run[t] - mref);
+    const float sb = __builtin_amdgcn_exp2f(mb - mref);
+    m_run[t] = mn;
+    l_run[t] = l_run[t] * sa + x[kWave] * sb;
+#pragma unroll
+    for (int d = 0; d < DTL; ++d)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[t][d][r] = o[t][d][r] * sa + x[(2 + 4 * d + r) * kWave] * sb;
   }
 
   // O^T lane (row col, grp) holds dims 16 d + 4 grp + r of query row col.
@@ -1890,16 +2004,7 @@ hipError_t launch_prefill_hd(PrefillArgs a, int64_t rows, hipStream_t st) {
   a.row_blocks = (int)((rows + BM - 1) / BM);
   const int64_t items = (int64_t)a.row_blocks * a.nkv * a.n_chunks;
   if (items > 0x7FFFFFFF) return hipErrorInvalidValue;
-  const void* kern = a.bs_shift >= 0 ? (const void*)&paged_prefill_kernel<DT, HD, true>
-                                     : (const void*)&paged_prefill_kernel<DT, HD, false>;
-  // Resident capacity (CUs x workgroups per CU) decides whether the halves pair up.
-  int dev = 0, cus = 0, per_cu = 0;
-  a.pair_halves = 0;
-  if (hipGetDevice(&dev) == hipSuccess &&
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, 0) == hipSuccess)
-    a.pair_halves = items <= (int64_t)cus * per_cu ? 1 : 0;
-  const dim3 grid((unsigned)items), block(256);
+  const dim3 grid((unsigned)items), block(512);
   if (a.bs_shift >= 0)
     hipLaunchKernelGGL((paged_prefill_kernel<DT, HD, true>), grid, block, 0, st, a);
   else
@@ -2233,7 +2338,6 @@ int pkv_paged_prefill_ex(void* out, int out_dtype, int64_t out_stride_tok, int64
   a.bs = block_size;
   a.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz(block_size) : -1;
   a.row_blocks = 0;  // set per head_dim by launch_prefill
-  a.pair_halves = 0;
   a.causal = causal != 0;
   a.q_rows = q_rows;
   a.lse = lse;
