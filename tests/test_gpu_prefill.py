@@ -83,6 +83,19 @@ def test_prefill_groups_and_block_sizes(nh, nkv, bs):
     assert (got - want).abs().max().item() <= ATOL
 
 
+@pytest.mark.parametrize(("hd", "bs"), [(256, 16), (64, 12), (128, 24), (32, 2)])
+def test_prefill_long_contexts_both_key_halves(hd, bs):
+    """Contexts of many key tiles, odd and even counts, split between the workgroup's
+    two key halves (the second half's tiles all past some rows' causal limit); block
+    sizes that are not powers of two take the per-lane gather path."""
+    _say("prefill long contexts", hd, bs)
+    spec = [(100, 491), (37, 300), (64, 64), (1, 1000), (130, 130)]
+    q, k, v, tables, ctx, cu = _chunks(spec, 8, 2, hd, bs, torch.bfloat16, seed=hd + bs)
+    got = _run(q, k, v, tables, ctx, cu, bs, 130)
+    want = oracle.prefill_attention(q, k, v, tables, cu, ctx, bs, threads=THREADS)
+    assert (got - want).abs().max().item() <= ATOL
+
+
 def _check_first_last(spec, q, k, v, tables, cu, got, bs):
     """The oracle on each chunk's first and last 16 query tokens (as their own sub-chunks
     with the same visible keys)."""
