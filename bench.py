@@ -63,6 +63,18 @@ def parse() -> argparse.Namespace:
     return ap.parse_args()
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (first 'model name' line of /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown CPU"
+
+
 def cpu_baseline(step, budget_s: float) -> dict:
     """The C oracle (double-accumulating scalar restatement of the reference's CPU
     gather-then-attention path) on the full config batch, OpenMP over host cores."""
@@ -87,7 +99,7 @@ def cpu_baseline(step, budget_s: float) -> dict:
         "kind": "port",
         "sample": f"full {step.name} layer-step (batch {step.batch}), median of {len(times)} "
                   f"reps; C oracle in float64, OpenMP {threads} threads, host "
-                  f"os.cpu_count()={os.cpu_count()}",
+                  f"os.cpu_count()={os.cpu_count()}, {cpu_model()}",
     }  # fmt: skip
 
 
