@@ -1543,9 +1543,9 @@ paged_prefill_kernel(const PrefillArgs a) {
     return (uint32_t)((((2 * d + c4 / 2) ^ SH::swz(tk)) * 16 + (c4 & 1) * 8) + tr * CH * 16);
   };
 
-  // S^T of a tile from its QK^T to its softmax, then in the same registers its P^T
-  // fragments until its P.V: 32-key step sg's hi and lo parts replace score blocks 2 sg
-  // and 2 sg + 1 (8 scores -> 8 operand words).
+  // S^T of a tile from its QK^T to its softmax, then in the same registers its
+  // probabilities P^T until its P.V (the first 32-key step's already packed as operand
+  // fragments: hi in block 0, lo in block 1).
   static_assert(NBETA == 2 * NSG, "two score blocks per P^T fragment pair");
   f32x4 sc[RT][NBETA];
 
@@ -1569,13 +1569,31 @@ paged_prefill_kernel(const PrefillArgs a) {
     }
   };
   // O^T += V^T . P^T of local tile m; each V^T fragment (two ds_read_b64_tr_b16
-  // transpose reads) serves every row tile.
+  // transpose reads) serves every row tile. P arrives as fp32 probabilities; each 32-key
+  // step packs its operand fragments here, in the matrix phase, whose VALU is otherwise
+  // idle (the softmax phase is the longer one).
   auto pv = [&](int m) __attribute__((always_inline)) {
     const char* vstage = reinterpret_cast<const char*>(&ring[half][1][m & 1][0]);
     const int l = fresh_lane();
 #pragma unroll
     for (int sg = 0; sg < NSG; ++sg) {
       if (sg) __builtin_amdgcn_sched_barrier(0);  // one 32-key step's fragments at a time
+      // P^T fragment of row tile t: the lane's own 8 probabilities (keys 32 sg + 16
+      // (e / 4) + 4 grp + e % 4), matching the transpose-read order of V^T. Step 0 was
+      // packed by the softmax; the later steps are packed here, while step 0's MFMAs run.
+      u32x4 phi[RT], plo[RT];
+#pragma unroll
+      for (int t = 0; t < RT; ++t) {
+        if (sg == 0) {
+          phi[t] = __builtin_bit_cast(u32x4, sc[t][0]);
+          plo[t] = __builtin_bit_cast(u32x4, sc[t][1]);
+        } else {
+          float p8[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) p8[e] = sc[t][2 * sg + e / 4][e % 4];
+          MMA::pack8(p8, phi[t], plo[t]);
+        }
+      }
 #pragma unroll
       for (int d = 0; d < DTL; ++d) {
         u32x4 vf;
@@ -1590,9 +1608,8 @@ paged_prefill_kernel(const PrefillArgs a) {
         }
 #pragma unroll
         for (int t = 0; t < RT; ++t) {
-          o[t][d] = MMA::mma(vf, __builtin_bit_cast(u32x4, sc[t][2 * sg]), o[t][d]);
-          if constexpr (MMA::kSplit)
-            o[t][d] = MMA::mma(vf, __builtin_bit_cast(u32x4, sc[t][2 * sg + 1]), o[t][d]);
+          o[t][d] = MMA::mma(vf, phi[t], o[t][d]);
+          if constexpr (MMA::kSplit) o[t][d] = MMA::mma(vf, plo[t], o[t][d]);
         }
       }
     }
@@ -1646,20 +1663,23 @@ paged_prefill_kernel(const PrefillArgs a) {
       const float mref = m_run[t] == -INFINITY ? 0.f : m_run[t];
       float psum = 0.f;
 #pragma unroll
-      for (int sg = 0; sg < NSG; ++sg) {
-        float p[8];
+      for (int beta = 0; beta < NBETA; ++beta)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          p[e] = __builtin_amdgcn_exp2f(
-              __builtin_fmaf(sc[t][2 * sg + e / 4][e % 4], a.scale_log2, -mref));
-          psum += p[e];
+        for (int r = 0; r < 4; ++r) {  // probabilities replace the scores
+          const float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[t][beta][r], a.scale_log2, -mref));
+          sc[t][beta][r] = pr;
+          psum += pr;
         }
-        // P^T fragment: the lane's own 8 probabilities (keys 32 sg + 16 (e / 4) + 4 grp
-        // + e % 4), matching the transpose-read order of V^T.
+      // The first 32-key step's P^T fragments are packed here (hi and lo into score
+      // blocks 0 and 1); P.V packs the others, balancing the two phases.
+      {
+        float p8[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) p8[e] = sc[t][e / 4][e % 4];
         u32x4 hi, lo;
-        MMA::pack8(p, hi, lo);
-        sc[t][2 * sg] = __builtin_bit_cast(f32x4, hi);
-        sc[t][2 * sg + 1] = __builtin_bit_cast(f32x4, lo);
+        MMA::pack8(p8, hi, lo);
+        sc[t][0] = __builtin_bit_cast(f32x4, hi);
+        sc[t][1] = __builtin_bit_cast(f32x4, lo);
       }
       l_run[t] += psum;
     }
