@@ -26,7 +26,8 @@ def paged_attention(layer_idx: int, q: torch.Tensor, k: torch.Tensor, v: torch.T
     head-major and transposes, layers.py:200). Appends k, v at ``batch.slot_mapping``
     (HIP append), then:
       * decode steps: the decode kernel over ``block_tables`` / ``context_lens``
-        (reference layers.py:201-212);
+        (reference layers.py:201-212), with cascade over shared prefixes when the batch
+        carries ``prefix_groups``;
       * mixed steps: decode rows through the decode kernel and prompt chunks through
         the chunked-prefill kernel (reference layers.py:227-266, where chunks go to
         FlashAttention varlen or per-chunk SDPA). Chunk shapes the prefill kernel does
@@ -39,7 +40,7 @@ def paged_attention(layer_idx: int, q: torch.Tensor, k: torch.Tensor, v: torch.T
     kc, vc, bs = cache.k[layer_idx], cache.v[layer_idx], cache.block_size
     if not batch.mixed:
         res = paged_decode_attention(q, kc, vc, batch.block_tables, batch.context_lens, bs,
-                                     out=out)  # fmt: skip
+                                     out=out, prefix_groups=batch.prefix_groups)  # fmt: skip
         return res.flatten(1)
     if out is None:
         out = torch.empty_like(q)

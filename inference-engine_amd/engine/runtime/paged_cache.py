@@ -203,6 +203,9 @@ class PagedBatch:
     row_tables: torch.Tensor | None = None  # [Tq, W] int32
     row_ctx: torch.Tensor | None = None  # [Tq] int32
     copy_pairs: torch.Tensor | None = None  # [n, 2] int64 (src, dst) copy-on-write
+    # Decode steps with cascade on: the groups of sequences sharing leading blocks
+    # (engine.kernels.paged_attention.PrefixGroups), or None.
+    prefix_groups: object | None = None
 
     @classmethod
     def build(
@@ -216,12 +219,20 @@ class PagedBatch:
         force_mixed: bool = False,
         copy_pairs: Sequence[tuple[int, int]] = (),
         device_slots: bool = False,
+        cascade: bool = False,
+        num_heads: int | None = None,
+        cascade_min_blocks: int = 16,
     ) -> PagedBatch:
         """Per sequence, in flattened order: its block table, its context length after
         this step (new tokens included) and its number of new tokens (reference :80-127).
         ``copy_pairs``: copy-on-write (src, dst) block pairs from the block manager, to
         apply before this step's writes. ``device_slots``: decode steps compute the slot
-        mapping on the device from the uploaded tables instead of on the host."""
+        mapping on the device from the uploaded tables instead of on the host.
+        ``cascade``: decode steps look for sequences whose tables start with the same
+        blocks (prompt prefixes shared through the prefix cache or a fork; at least
+        ``cascade_min_blocks`` of them, fully covered) and attend to each shared prefix
+        once per group (``paged_decode_attention(prefix_groups=)``); needs the model's
+        ``num_heads``."""
         if not use_kernel:
             raise ValueError("PagedBatch: this build has only the kernel path (HIP)")
         if not query_lens:
@@ -231,6 +242,14 @@ class PagedBatch:
             pairs = torch.tensor(list(copy_pairs), dtype=torch.int64).view(-1, 2).to(device)
         if max(query_lens) == 1 and not force_mixed:
             batch = cls._decode(cache, block_tables, context_lens, device, device_slots)
+            if cascade:
+                if num_heads is None:
+                    raise ValueError("PagedBatch: cascade needs the model's num_heads")
+                from engine.kernels.paged_attention import find_prefix_groups
+
+                batch.prefix_groups = find_prefix_groups(
+                    cls._tables(block_tables), list(context_lens), cache.block_size,
+                    num_heads, cache.k.shape[2], device, min_blocks=cascade_min_blocks)  # fmt: skip
         else:
             batch = cls._mixed(cache, block_tables, context_lens, query_lens, device)
         batch.copy_pairs = pairs

@@ -83,6 +83,25 @@ def test_paged_batch_metadata_matches_definitions():
         PagedBatch.build(cache, [[1]], [2], [1], "cpu", use_kernel=False)
 
 
+def test_paged_batch_cascade_groups():
+    """Decode steps with cascade: sequences whose tables start with the same blocks get
+    prefix groups (their shared blocks, fully covered); nothing shared: none."""
+    cfg = TinyConfig()
+    cache = PagedKVCache(cfg, 32, 4, "cpu", torch.float32)
+    shared = [1, 2, 3]
+    tables = [shared + [10, 11], shared + [12], [20, 21, 22, 23]]
+    b = PagedBatch.build(cache, tables, [18, 14, 15], [1, 1, 1], "cpu", cascade=True,
+                         num_heads=cfg.num_attention_heads, cascade_min_blocks=2)  # fmt: skip
+    pg = b.prefix_groups
+    assert pg is not None and pg.members == 2
+    assert pg.first_block.tolist() == [3, 3, 0] and pg.prefix_row.tolist()[2] == -1
+    none = PagedBatch.build(cache, tables[2:], [15], [1], "cpu", cascade=True,
+                            num_heads=cfg.num_attention_heads, cascade_min_blocks=2)  # fmt: skip
+    assert none.prefix_groups is None
+    with pytest.raises(ValueError):
+        PagedBatch.build(cache, tables, [18, 14, 15], [1, 1, 1], "cpu", cascade=True)
+
+
 @pytest.mark.parametrize("budget", [4096, 8])
 def test_engine_reference_backend_matches_static_loop(budget):
     model = _model()
@@ -174,6 +193,28 @@ def test_engine_kernels_match_reference_backend_16bit(dtype, hd, bs):
                  torch.stack(runs["reference"][1].logits[r])).abs().max().item()
                 for r in PROMPTS)  # fmt: skip
     assert worst <= 0.05, worst  # 16-bit activations: a few ulps of the logits
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_engine_cascade_decode_matches_plain(dtype):
+    """Decode steps with cascade over prompt prefixes shared through the prefix cache:
+    the plain decode's tokens, logits within 16-bit rounding."""
+    from tiny_llama import KernelBackend
+
+    model = _cuda_model(dtype)
+    prompts = {"b": SHARED + [1, 2], "d": SHARED + [3], "f": SHARED, "g": SHARED + [4, 5, 6]}
+    runs = {}
+    for min_blocks in (None, 2):
+        eng = TinyEngine(model, KernelBackend(), num_blocks=64, block_size=4,
+                         cascade_min_blocks=min_blocks)  # fmt: skip
+        runs[min_blocks] = (_run_staggered(eng, prompts, 12), eng)
+    assert any(s["cascade"] for s in runs[2][1].log)
+    assert runs[2][0] == runs[None][0]
+    worst = max((torch.stack(runs[2][1].logits[r]) -
+                 torch.stack(runs[None][1].logits[r])).abs().max().item()
+                for r in prompts)  # fmt: skip
+    assert worst <= 0.05, worst
 
 
 @pytest.mark.gpu

@@ -276,7 +276,8 @@ class TinyEngine:
     def __init__(self, model: TinyLlama, backend, num_blocks: int = 64, block_size: int = 4,
                  max_num_seqs: int = 8, max_num_batched_tokens: int = 4096,
                  enable_prefix_caching: bool = True, graphs: bool = False,
-                 mixed_graphs: bool = False, debug_checks: bool = True) -> None:  # fmt: skip
+                 mixed_graphs: bool = False, debug_checks: bool = True,
+                 cascade_min_blocks: int | None = None) -> None:  # fmt: skip
         self.model, self.backend = model, backend
         w = model.embed.weight
         self.device, self.dtype = w.device, w.dtype
@@ -285,6 +286,8 @@ class TinyEngine:
         self.bm = BlockManager(num_blocks, block_size, enable_prefix_caching)
         self.max_num_seqs, self.budget = max_num_seqs, max_num_batched_tokens
         self.debug_checks = debug_checks
+        # eager decode steps: cascade over prefixes of at least this many shared blocks
+        self.cascade_min_blocks = cascade_min_blocks
         self.waiting: list[Seq] = []
         self.running: list[Seq] = []
         self.done: dict[str, list[int]] = {}
@@ -377,7 +380,10 @@ class TinyEngine:
             logits = self.mixed_graphs.run(ids, positions, batch)[:, 0]
             used_mixed_graph = True
         else:
-            batch = PagedBatch.build(self.cache, tables, ctx, qlens, self.device)
+            cascade = self.cascade_min_blocks is not None
+            batch = PagedBatch.build(self.cache, tables, ctx, qlens, self.device,
+                                     cascade=cascade, num_heads=self.model.cfg.num_attention_heads,
+                                     cascade_min_blocks=self.cascade_min_blocks or 16)  # fmt: skip
             logits = self.model(torch.tensor([ids], device=self.device),
                                 torch.tensor([positions], device=self.device), batch)[:, 0]  # fmt: skip
         greedy = logits.argmax(-1).tolist()
@@ -398,9 +404,10 @@ class TinyEngine:
                 self.done[seq.rid] = seq.out
         if self.debug_checks:
             self.bm.check_no_leaks()
+        cascaded = not (used_graph or used_mixed_graph) and batch.prefix_groups is not None
         self.log.append({"seqs": len(plan), "tokens": len(ids), "decode_only": decode_only,
                          "graph": used_graph, "mixed_graph": used_mixed_graph,
-                         "copies": len(pairs)})  # fmt: skip
+                         "copies": len(pairs), "cascade": cascaded})  # fmt: skip
         return outputs
 
     def generate(self, prompts: dict[str, list[int]], max_tokens: int) -> dict[str, list[int]]:
