@@ -55,8 +55,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-graph", action="store_true", help="time eager calls only")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--only", choices=["cascade"], default=None,
-                    help="time only cascade decode (config c3), e.g. under a profiler")
+    ap.add_argument("--only", choices=["cascade", "cow", "append"], default=None,
+                    help="time one part alone, e.g. under a profiler: cascade decode or "
+                         "the copy-on-write (config c3), the KV append (config c5)")  # fmt: skip
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 5 plain 1 GiB device-to-device copies: the known-size "
                          "kernel that scales rocprofv3's FETCH_SIZE / WRITE_SIZE")  # fmt: skip
@@ -300,6 +301,23 @@ def bench_cow(torch, step, layers: int = 28, blocks: int = 2048) -> dict:
             "cow_unique_gbps": round(unique / (us * 1e-6) / 1e9, 1)}
 
 
+def bench_append(args, torch) -> dict:
+    """Config 5's KV append alone (2,168 new rows into the 8B-shaped pool), graph replay."""
+    from engine import workloads
+    from engine.runtime.paged_cache import kv_append
+
+    m = workloads.config5(torch.device("cuda:0"), seed=args.seed)
+
+    def append():
+        kv_append(m.k_cache, m.v_cache, m.new_k, m.new_v, m.slot_mapping)
+
+    us = graph_us(torch, [append] * 8, 8 * args.steps, args.warmup)[0]
+    nbytes = 2 * m.new_k.numel() * m.new_k.element_size() * 2  # K and V, read + written
+    return {"config": {"workload": m.name, "rows": int(m.slot_mapping.numel())},
+            "append_us": round(us, 2), "append_bytes": nbytes,
+            "append_gbps": round(nbytes / (us * 1e-6) / 1e9, 1)}  # fmt: skip
+
+
 def bench_mixed(args, torch) -> dict:
     from engine import workloads
     from engine.kernels import paged_attention as pa
@@ -380,14 +398,19 @@ def main() -> int:
 
     import torch
 
+    need = {"cascade": "c3", "cow": "c3", "append": "c5"}.get(args.only)
+    if need and args.config != need:
+        print(f"bench.py: --only {args.only} needs --config {need}", file=sys.stderr)
+        return 2
     if args.only == "cascade":
-        if args.config != "c3":
-            print("bench.py: --only cascade needs --config c3 (the shared-prefix batch)",
-                  file=sys.stderr)  # fmt: skip
-            return 2
         step, pools, out, wgs = decode_setup(args, torch)
         line = {"config": {"workload": step.name, "layer_pools": len(pools)},
                 **bench_cascade(args, torch, step, pools, out, wgs, step.unique_kv_bytes())}
+    elif args.only == "cow":
+        step, _, _, _ = decode_setup(args, torch)
+        line = {"config": {"workload": step.name}, **bench_cow(torch, step)}
+    elif args.only == "append":
+        line = bench_append(args, torch)
     elif args.config == "c5":
         line = bench_mixed(args, torch)
     else:
