@@ -1,0 +1,1129 @@
+// decode.hip -- split-K (stream-K) paged decode attention, its combine pass, and cascade
+// decode's tail pass and merge (include/paged_kv.h: pkv_paged_decode*).
+
+#include "common.h"
+
+namespace {
+
+using namespace pkv;
+
+// ---------------------------------------------------------------------------------
+// Paged decode attention: stream-K pass.
+//
+// The contexts of all sequences are cut into units of TILE tokens (a sequence with an
+// empty context owns one unit) and laid end to end, sequence by sequence. The grid has
+// exactly as many workgroups along x as the GPU holds at once, and workgroup w takes
+// the contiguous unit range [w*U/G, (w+1)*U/G): every CU streams the same number of
+// K/V bytes whatever the context lengths, and since workgroups are dealt to the 8 XCDs
+// round-robin, so does every XCD. A sequence that lies wholly inside one range gets its
+// output written directly; a sequence cut by a range boundary leaves one (m, l, acc)
+// record per piece (at most two per workgroup: its first and its last piece), which the
+// combine pass merges. Ranges are computed on the device from context_lens, so the
+// launch shape depends only on static shapes and one hipGraph serves every length.
+//
+// One wave = one KV head (and up to GPW of its query heads). A workgroup holds the
+// waves of consecutive KV heads over the same unit range, so together they stream each
+// block's whole [block_size, nkv, hd] span, which is contiguous. Inside a wave a K/V row
+// of hd elements is LPT lanes x 16 bytes; one 16-byte load per lane covers TPL = 64/LPT
+// tokens, and a tile is NLOAD such loads. The next tile's K and V loads are issued
+// before the current tile is reduced.
+// ---------------------------------------------------------------------------------
+
+template <int DT, int HD> struct DecodeShape {
+  static constexpr int VEC = vec16<DT>();
+  static constexpr int LPT = HD / VEC;
+  static constexpr int TPL = kWave / LPT;
+  static constexpr int NLOAD = (16 / TPL) < 1 ? 1
+                               : ((16 / TPL) > PKV_DECODE_NLOAD_MAX ? PKV_DECODE_NLOAD_MAX
+                                                                   : 16 / TPL);
+  static constexpr int TILE = NLOAD * TPL;
+  static_assert(LPT >= 1 && LPT <= kWave, "head_dim out of range");
+};
+
+struct DecodeArgs {
+  void* out;
+  int64_t out_sb, out_sh;
+  const void* q;
+  int64_t q_sb, q_sh;
+  const void* k;
+  const void* v;
+  int64_t kv_ss, kv_sh, num_slots;
+  const int32_t* tables;
+  int64_t table_stride;
+  int32_t max_blocks;
+  const int32_t* ctx;
+  int32_t batch, nh, nkv, groups, nsub, bs, bs_shift;  // bs_shift < 0: block_size not pow2
+  int32_t unit_tokens;  // TILE of the instantiated kernel
+  int32_t num_wg;       // workgroups along x sharing the unit stream
+  float scale_log2;     // scale * log2(e)
+  int4* desc;           // [batch] per-sequence merge plan (see SeqDesc)
+  float* ws_acc;        // [num_wg, 2, nh, HD] partial records
+  float* ws_ml;         // [num_wg, 2, nh, 2]   their (max, sum)
+  int out_f32;
+  const int32_t* first_block;  // [batch] or null: attend from table column first_block[b]
+  float* lse;                  // [batch, nh] or null: log2 of each softmax's normaliser
+  // Cascade (pre_row non-null): normalised attentions of the same queries over other
+  // keys (a shared prefix's pieces), merged into the result by the combine pass. Part k
+  // of sequence b is row pre_row[b] + k * pre_stride of pre_o [rows, nh, HD] / pre_lse
+  // [rows, nh] (pre_row[b] < 0: none). The stream pass then writes the sequences it
+  // finishes to out / lse as fp32 scratch, and the combine pass writes every sequence's
+  // result to fin (fin_f32: fp32, else DT) and its normaliser to fin_lse (if non-null).
+  const float* pre_o;
+  const float* pre_lse;
+  const int32_t* pre_row;
+  int32_t pre_parts;
+  int64_t pre_stride;
+  void* fin;
+  int64_t fin_sb, fin_sh;
+  int fin_f32;
+  float* fin_lse;
+};
+
+// Table column sequence b starts from (a shared prefix handled elsewhere is skipped).
+__device__ __forceinline__ int first_blk(const DecodeArgs& a, int b) {
+  if (!a.first_block) return 0;
+  const int f = a.first_block[b];
+  return f < 0 ? 0 : (f > a.max_blocks ? a.max_blocks : f);
+}
+
+// Tokens sequence b attends to, clamped: 0 <= n <= (max_blocks - first) * block_size.
+// They are positions first * block_size + p, p < n.
+__device__ __forceinline__ int clamped_ctx(const DecodeArgs& a, int b) {
+  const int fb = first_blk(a, b);
+  const int n = a.ctx[b] - fb * a.bs;
+  const int cap = (a.max_blocks - fb) * a.bs;
+  return n < 0 ? 0 : (n > cap ? cap : n);
+}
+
+// Log2 of the softmax normaliser in the kernel's score units (scores x scale x log2 e):
+// max + log2(sum of exp2(score - max)); -inf when no key was live.
+__device__ __forceinline__ float lse_of(float m, float l) {
+  return l > 0.f ? m + __log2f(l) : -INFINITY;
+}
+
+// Folds sequence b's prefix parts for head h into a wave's running softmax state (m, l,
+// acc), lane holding head dims lane + 64 c (c < DPL; dims >= HD skipped). A part is a
+// normalised output O_k with log2 normaliser lse_k, i.e. the state (lse_k, 1, O_k):
+// with M the new max, l <- l 2^(m - M) + sum_k 2^(lse_k - M) and likewise acc. Parts
+// are loaded eight at a time, every load issued before any is used.
+template <int HD, int DPL>
+__device__ __forceinline__ void fold_prefix(const DecodeArgs& a, int b, int h, float& m,
+                                            float& l, float (&acc)[DPL]) {
+  const int r = a.pre_row[b];
+  if (r < 0) return;
+  const int lane = threadIdx.x & (kWave - 1);
+  constexpr int C = 8;
+  for (int k0 = 0; k0 < a.pre_parts; k0 += C) {
+    float lk[C], x[C][DPL];
+#pragma unroll
+    for (int jj = 0; jj < C; ++jj) {
+      const int k = k0 + jj;
+      const bool live = k < a.pre_parts;
+      const int64_t row = ((int64_t)r + (int64_t)(live ? k : 0) * a.pre_stride) * a.nh + h;
+      lk[jj] = live ? a.pre_lse[row] : -INFINITY;
+      const float* p = a.pre_o + row * HD;
+#pragma unroll
+      for (int c = 0; c < DPL; ++c) x[jj][c] = lane + kWave * c < HD ? p[lane + kWave * c] : 0.f;
+    }
+    float mn = m;
+#pragma unroll
+    for (int jj = 0; jj < C; ++jj) mn = fmaxf(mn, lk[jj]);
+    const float mref = mn == -INFINITY ? 0.f : mn;  // nothing live yet: weights 0
+    const float alpha = __builtin_amdgcn_exp2f(m - mref);
+    m = mn;
+    l *= alpha;
+#pragma unroll
+    for (int c = 0; c < DPL; ++c) acc[c] *= alpha;
+#pragma unroll
+    for (int jj = 0; jj < C; ++jj) {
+      const float wj = __builtin_amdgcn_exp2f(lk[jj] - mref);  // dead or empty: 0
+      l += wj;
+#pragma unroll
+      for (int c = 0; c < DPL; ++c) acc[c] = __builtin_fmaf(wj, x[jj][c], acc[c]);
+    }
+  }
+}
+
+__device__ __forceinline__ int units_of(const DecodeArgs& a, int n) {
+  return n == 0 ? 1 : (n + a.unit_tokens - 1) / a.unit_tokens;
+}
+
+// Wave-wide walk over the unit prefix sums. With target >= 0 returns the sequence b
+// that owns unit `target` and its first unit in *ustart; with target < 0 (or past the
+// end) returns batch and the total unit count in *ustart. Call from whole waves.
+__device__ int find_unit(const DecodeArgs& a, int64_t target, int64_t* ustart) {
+  const int lane = threadIdx.x & (kWave - 1);
+  int64_t base = 0;
+  for (int c0 = 0; c0 < a.batch; c0 += kWave) {
+    const int bb = c0 + lane;
+    const int cnt = bb < a.batch ? units_of(a, clamped_ctx(a, bb)) : 0;
+    int incl = cnt;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const int t = __shfl_up(incl, off);
+      if (lane >= off) incl += t;
+    }
+    const int chunk_total = __shfl(incl, kWave - 1);
+    if (target >= 0 && target < base + chunk_total) {
+      const unsigned long long hit = __ballot(base + incl > target);
+      const int l = __ffsll((long long)hit) - 1;
+      *ustart = base + __shfl(incl - cnt, l);
+      return c0 + l;
+    }
+    base += chunk_total;
+  }
+  *ustart = base;
+  return a.batch;
+}
+
+__device__ __forceinline__ int64_t range_start(int64_t w, int64_t units, int64_t wgs) {
+  return w * units / wgs;
+}
+// The workgroup whose range holds unit u: the largest w with range_start(w) <= u.
+__device__ __forceinline__ int64_t wg_of_unit(int64_t u, int64_t units, int64_t wgs) {
+  return ((u + 1) * wgs - 1) / units;
+}
+
+// Merge plan of one sequence, written by the workgroup that holds its first unit (so
+// every sequence gets exactly one, every call): the first workgroup w0 of its pieces,
+// the number of workgroups w0..w1 it spans (1: written directly), the record slot its
+// piece has in w0, and whether every range is non-empty (units >= workgroups).
+__device__ __forceinline__ void write_desc(const DecodeArgs& a, int b, int w, int64_t ub,
+                                           int64_t ue, int64_t rs, int64_t total) {
+  if (!a.desc) return;
+  const int64_t w1 = wg_of_unit(ue - 1, total, a.num_wg);
+  a.desc[b] = make_int4(w, (int)(w1 - w + 1), rs < ub ? 1 : 0, total >= a.num_wg ? 1 : 0);
+}
+
+template <int DT, int HD, int GPW>
+__global__ void __launch_bounds__(512)
+paged_decode_stream_kernel(const DecodeArgs a) {
+  using Sh = DecodeShape<DT, HD>;
+  constexpr int VEC = Sh::VEC, LPT = Sh::LPT, TPL = Sh::TPL, NLOAD = Sh::NLOAD;
+  constexpr int TILE = Sh::TILE;
+  using S = typename Elt<DT>::S;
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int task = blockIdx.y * (blockDim.x / kWave) + (threadIdx.x / kWave);
+  const int kvh = task / a.nsub;
+  if (kvh >= a.nkv) return;
+  const int h0 = kvh * a.groups + (task - kvh * a.nsub) * GPW;
+  const int w = blockIdx.x;
+
+  int64_t total;
+  find_unit(a, -1, &total);
+  const int64_t rs = range_start(w, total, a.num_wg);
+  const int64_t re = range_start(w + 1, total, a.num_wg);
+  if (rs >= re) return;
+  int64_t ub;
+  int b = find_unit(a, rs, &ub);
+
+  const int row = lane / LPT;         // token sub-index inside a load
+  const int d0 = (lane % LPT) * VEC;  // this lane's first head_dim element
+  const S* kbase = reinterpret_cast<const S*>(a.k) + (int64_t)kvh * a.kv_sh + d0;
+  const S* vbase = reinterpret_cast<const S*>(a.v) + (int64_t)kvh * a.kv_sh + d0;
+
+  for (int64_t u = rs; u < re && b < a.batch; ++b) {
+    const int n = clamped_ctx(a, b);
+    const int64_t ue = ub + units_of(a, n);
+    const int64_t seg_end = ue < re ? ue : re;
+    const bool whole = (u == ub) && (seg_end == ue);
+    const int slot = (u == rs) ? 0 : 1;  // which record a cut piece goes to
+    const int t0 = (int)(u - ub) * a.unit_tokens;
+    const int t1 = min(n, (int)(seg_end - ub) * a.unit_tokens);
+    if (u == ub && task == 0 && lane == 0) write_desc(a, b, w, ub, ue, rs, total);
+    u = seg_end;
+    ub = ue;
+
+    // Query rows of this wave for sequence b, pre-scaled into the exp2 domain.
+    float qf[GPW][VEC];
+#pragma unroll
+    for (int g = 0; g < GPW; ++g) {
+      const S* qp = reinterpret_cast<const S*>(a.q) + b * a.q_sb + (int64_t)(h0 + g) * a.q_sh + d0;
+      float t[VEC];
+      unpack16<DT>(*reinterpret_cast<const uint4*>(qp), t);
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) qf[g][i] = t[i] * a.scale_log2;
+    }
+
+    // Block ids of up to 64 consecutive blocks starting at cb, one per lane.
+    int cb = 0, tbl = 0;
+    const int fb = first_blk(a, b);
+    auto load_table = [&](int first_block) {
+      cb = first_block;
+      const int j = cb + lane;
+      tbl = j < a.max_blocks - fb ? a.tables[b * a.table_stride + fb + j] : 0;
+    };
+    auto block_of = [&](int p) { return a.bs_shift >= 0 ? (p >> a.bs_shift) : p / a.bs; };
+
+    // Slot of this lane's token in load i of the tile starting at tb (-1: masked).
+    auto slot_of = [&](int tb, int i) -> int64_t {
+      const int p = tb + i * TPL + row;
+      const int blk = block_of(p);
+      const int bid = __shfl(tbl, blk - cb);
+      const int off = p - blk * a.bs;
+      const int64_t sl = (int64_t)bid * a.bs + off;
+      return (p < t1 && sl >= 0 && sl < a.num_slots) ? sl : (int64_t)-1;
+    };
+    // Issue the K/V loads of the tile at tb (first making sure the table window
+    // covers it); bit i of the result: load i holds a live token for this lane.
+    auto load_tile = [&](int tb, uint4* kr, uint4* vr) -> unsigned {
+      if (tb < t1 && block_of(min(tb + TILE, t1) - 1) - cb >= kWave) load_table(block_of(tb));
+      unsigned ok = 0;
+#pragma unroll
+      for (int i = 0; i < NLOAD; ++i) {
+        const int64_t sl = slot_of(tb, i);
+        uint4 kk = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
+        if (sl >= 0) {
+          kk = load_kv16(kbase + sl * a.kv_ss);
+          vv = load_kv16(vbase + sl * a.kv_ss);
+          ok |= 1u << i;
+        }
+        kr[i] = kk;
+        vr[i] = vv;
+      }
+      return ok;
+    };
+
+    float m[GPW], l[GPW], acc[GPW][VEC];
+#pragma unroll
+    for (int g = 0; g < GPW; ++g) {
+      m[g] = -INFINITY;
+      l[g] = 0.f;
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) acc[g][i] = 0.f;
+    }
+
+    if (t0 < t1) {
+      load_table(block_of(t0));
+      uint4 kc[NLOAD], vc[NLOAD];
+      unsigned okc = load_tile(t0, kc, vc);
+      for (int tb = t0; tb < t1; tb += TILE) {
+        uint4 kn[NLOAD], vn[NLOAD];
+        const unsigned okn = load_tile(tb + TILE, kn, vn);  // past t1 every lane is masked
+
+        float sc[NLOAD][GPW];
+#pragma unroll
+        for (int i = 0; i < NLOAD; ++i) {
+          float kf[VEC];
+          unpack16<DT>(kc[i], kf);
+#pragma unroll
+          for (int g = 0; g < GPW; ++g) {
+            float d = 0.f;
+#pragma unroll
+            for (int c = 0; c < VEC; ++c) d = __builtin_fmaf(qf[g][c], kf[c], d);
+            sc[i][g] = group_sum<LPT>(d);
+          }
+        }
+#pragma unroll
+        for (int g = 0; g < GPW; ++g) {
+          float mx = -INFINITY;
+#pragma unroll
+          for (int i = 0; i < NLOAD; ++i) {
+            sc[i][g] = ((okc >> i) & 1u) ? sc[i][g] : -INFINITY;
+            mx = fmaxf(mx, sc[i][g]);
+          }
+          mx = across_max<LPT>(mx);
+          const float mn = fmaxf(m[g], mx);
+          // While every token so far is masked the max is -inf; exponents are then
+          // taken against 0 so exp2(-inf - -inf) never turns the empty state into NaN.
+          const float mref = mn == -INFINITY ? 0.f : mn;
+          const float alpha = __builtin_amdgcn_exp2f(m[g] - mref);
+          m[g] = mn;
+          l[g] *= alpha;
+#pragma unroll
+          for (int c = 0; c < VEC; ++c) acc[g][c] *= alpha;
+#pragma unroll
+          for (int i = 0; i < NLOAD; ++i) sc[i][g] = __builtin_amdgcn_exp2f(sc[i][g] - mref);
+        }
+#pragma unroll
+        for (int i = 0; i < NLOAD; ++i) {
+          float vf[VEC];
+          unpack16<DT>(vc[i], vf);
+#pragma unroll
+          for (int g = 0; g < GPW; ++g) {
+            l[g] += sc[i][g];
+#pragma unroll
+            for (int c = 0; c < VEC; ++c) acc[g][c] = __builtin_fmaf(sc[i][g], vf[c], acc[g][c]);
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < NLOAD; ++i) {
+          kc[i] = kn[i];
+          vc[i] = vn[i];
+        }
+        okc = okn;
+      }
+    }
+
+    // Combine the TPL token rows of the wave.
+#pragma unroll
+    for (int g = 0; g < GPW; ++g) {
+      l[g] = across_sum<LPT>(l[g]);
+#pragma unroll
+      for (int c = 0; c < VEC; ++c) acc[g][c] = across_sum_exact<LPT>(acc[g][c]);
+    }
+
+    if (lane < LPT) {
+      if (whole) {  // the whole context was in this range: final output directly
+#pragma unroll
+        for (int g = 0; g < GPW; ++g) {
+          // no live token (empty context): 0, the reference oracle's einsum over no keys
+          const float inv = l[g] > 0.f ? 1.f / l[g] : 0.f;
+          float o[VEC];
+#pragma unroll
+          for (int c = 0; c < VEC; ++c) o[c] = acc[g][c] * inv;
+          const int64_t e = b * a.out_sb + (int64_t)(h0 + g) * a.out_sh + d0;
+          if (a.out_f32) store_vec<PKV_F32, VEC>((float*)a.out + e, o);
+          else store_vec<DT, VEC>((S*)a.out + e, o);
+          if (a.lse && lane == 0) a.lse[(int64_t)b * a.nh + h0 + g] = lse_of(m[g], l[g]);
+        }
+      } else {
+#pragma unroll
+        for (int g = 0; g < GPW; ++g) {
+          const int64_t rec = ((int64_t)w * 2 + slot) * a.nh + h0 + g;
+          store_vec<PKV_F32, VEC>(a.ws_acc + rec * HD + d0, acc[g]);
+          if (lane == 0) *reinterpret_cast<float2*>(a.ws_ml + 2 * rec) = make_float2(m[g], l[g]);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// MFMA variant of the stream pass for 16-bit K/V at head_dim 128 (the Llama-3 shapes).
+//
+// Same stream-K ranges, records and outputs as paged_decode_stream_kernel; only the
+// per-tile arithmetic differs. A tile is 16 tokens. Lane l is (col = l % 16, grp =
+// l / 16).
+//   * Scores on the matrix cores: S[16 tokens x 16 cols] = K_tile . Q^T with four
+//     v_mfma_f32_16x16x32 (32 head dims each). A operand: lane (t, g) holds K[token t]
+//     dims 32m + 8g .. +8 (one 16-byte load per MFMA); B operand: lane (j, g) holds
+//     Q[head j] at the same dims (zero for j >= GPW). Result: lane (j, g) holds the
+//     scores of tokens 4g + r (r < 4) for query head j.
+//   * Softmax in that layout: per-head max over the 16 tokens with two permlane swaps
+//     (v_permlane16/32_swap give {x[l], x[l^16]} / {x[l], x[l^32]}: no LDS trip).
+//   * PV on the VALU in fp32: lane (c, g) holds V[token 4g + r] dims 8c .. +8; each
+//     head's probabilities reach it with DPP row_newbcast (lane h of each 16-lane row
+//     to the whole row), since token 4g + r's score sits in lane (h, g) of that row.
+// When block_size is a multiple of 16 a tile lies inside one block: its block id is
+// read with v_readlane into a scalar and every lane's address is a fixed offset from it.
+// ---------------------------------------------------------------------------------
+
+
+
+template <int DT> struct Mfma16x16x32;
+template <> struct Mfma16x16x32<PKV_BF16> {
+  typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+  __device__ static f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8, a),
+                                                   __builtin_bit_cast(v8, b), c, 0, 0, 0);
+  }
+};
+template <> struct Mfma16x16x32<PKV_F16> {
+  typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+  __device__ static f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8, a),
+                                                  __builtin_bit_cast(v8, b), c, 0, 0, 0);
+  }
+};
+
+__device__ __forceinline__ u32x4 load_kv16v(const void* p) {
+#if PKV_DECODE_STREAM_LOADS
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+#else
+  return *reinterpret_cast<const u32x4*>(p);
+#endif
+}
+
+template <int DT> __device__ __forceinline__ void unpack16v(u32x4 r, float* f) {
+  unpack16<DT>(make_uint4(r.x, r.y, r.z, r.w), f);
+}
+
+
+template <int DT, int GPW, bool FAST>
+__global__ void __launch_bounds__(512)
+paged_decode_mfma_kernel(const DecodeArgs a) {
+  constexpr int HD = 128, TILE = 16;
+  static_assert(GPW >= 1 && GPW <= 4, "at most 4 query heads per wave");
+  using S = typename Elt<DT>::S;
+  using MMA = Mfma16x16x32<DT>;
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int task = blockIdx.y * (blockDim.x / kWave) + (threadIdx.x / kWave);
+  const int kvh = task / a.nsub;
+  if (kvh >= a.nkv) return;
+  const int h0 = kvh * a.groups + (task - kvh * a.nsub) * GPW;
+  const int w = blockIdx.x;
+
+  int64_t total;
+  find_unit(a, -1, &total);
+  const int64_t rs = range_start(w, total, a.num_wg);
+  const int64_t re = range_start(w + 1, total, a.num_wg);
+  if (rs >= re) return;
+  int64_t ub;
+  int b = find_unit(a, rs, &ub);
+
+  const int col = lane & 15, grp = lane >> 4;
+  // FAST: block_size is a multiple of 16, so a tile never crosses a block.
+  const S* kbase = reinterpret_cast<const S*>(a.k) + (int64_t)kvh * a.kv_sh;
+  const S* vbase = reinterpret_cast<const S*>(a.v) + (int64_t)kvh * a.kv_sh;
+  // Fixed per-lane element offsets from a tile's first slot (fast path).
+  const int64_t k_off = col * a.kv_ss + 8 * grp;
+  int64_t v_off[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) v_off[r] = (4 * grp + r) * a.kv_ss + 8 * col;
+
+  for (int64_t u = rs; u < re && b < a.batch; ++b) {
+    const int n = clamped_ctx(a, b);
+    const int64_t ue = ub + units_of(a, n);
+    const int64_t seg_end = ue < re ? ue : re;
+    const bool whole = (u == ub) && (seg_end == ue);
+    const int slot = (u == rs) ? 0 : 1;
+    const int t0 = (int)(u - ub) * TILE;
+    const int t1 = min(n, (int)(seg_end - ub) * TILE);
+    if (u == ub && task == 0 && lane == 0) write_desc(a, b, w, ub, ue, rs, total);
+    u = seg_end;
+    ub = ue;
+
+    // Q^T as the B operand: column col = query head h0 + col.
+    u32x4 qb[4];
+    {
+      const S* qp = reinterpret_cast<const S*>(a.q) + b * a.q_sb + (int64_t)(h0 + col) * a.q_sh + 8 * grp;
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+        qb[m] = col < GPW ? *reinterpret_cast<const u32x4*>(qp + 32 * m) : u32x4{0, 0, 0, 0};
+    }
+
+    int cb = 0, tbl = 0;
+    const int fb = first_blk(a, b);
+    auto load_table = [&](int first_block) {
+      cb = first_block;
+      const int j = cb + lane;
+      tbl = j < a.max_blocks - fb ? a.tables[b * a.table_stride + fb + j] : 0;
+    };
+    auto block_of = [&](int p) { return a.bs_shift >= 0 ? (p >> a.bs_shift) : p / a.bs; };
+
+    // Issue a tile's K (MFMA A layout) and V (row layout) loads; returns, per lane,
+    // bit r set when token 4*grp + r of the tile is live.
+    auto load_tile = [&](int tb, u32x4* kr, u32x4* vr) -> unsigned {
+      const u32x4 z = {0, 0, 0, 0};
+      if (tb >= t1) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kr[i] = vr[i] = z;
+        return 0;
+      }
+      if (block_of(min(tb + TILE, t1) - 1) - cb >= kWave) load_table(block_of(tb));
+      unsigned ok = 0;
+      if constexpr (FAST) {
+        const int blk = block_of(tb);
+        const int bid = __builtin_amdgcn_readlane(tbl, blk - cb);
+        const int64_t slot0 = (int64_t)bid * a.bs + (tb - blk * a.bs);
+        const int live = (bid >= 0 && slot0 + TILE <= a.num_slots) ? min(TILE, t1 - tb) : 0;
+        const S* kt = kbase + slot0 * a.kv_ss;
+        const S* vt = vbase + slot0 * a.kv_ss;
+        if (live == TILE) {  // full tile: every lane loads, no predication
+#pragma unroll
+          for (int m = 0; m < 4; ++m) kr[m] = load_kv16v(kt + k_off + 32 * m);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) vr[r] = load_kv16v(vt + v_off[r]);
+          return 0xFu;
+        }
+        if (live == 0) {  // block id outside the pool: the tile is masked
+#pragma unroll
+          for (int i = 0; i < 4; ++i) kr[i] = vr[i] = z;
+          return 0;
+        }
+        // Last, partial tile of a piece: lanes past the end re-read the last live
+        // token (finite data) and are masked out of the softmax (P = 0).
+        const int kt_tok = min(col, live - 1);
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+          kr[m] = load_kv16v(kt + kt_tok * a.kv_ss + 8 * grp + 32 * m);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int tok = 4 * grp + r;
+          vr[r] = load_kv16v(vt + min(tok, live - 1) * a.kv_ss + 8 * col);
+          ok |= (unsigned)(tok < live) << r;
+        }
+      } else {
+        // K token tb + col; the V lanes fetch their tokens' slots from those lanes.
+        const int p = tb + col;
+        const int blk = block_of(p);
+        const int bid = __shfl(tbl, blk - cb);
+        const int64_t sl = (int64_t)bid * a.bs + (p - blk * a.bs);
+        const bool kon = p < t1 && sl >= 0 && sl < a.num_slots;
+        const int64_t kslot = kon ? sl : -1;
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+          kr[m] = kon ? load_kv16v(kbase + kslot * a.kv_ss + 8 * grp + 32 * m) : z;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int src = 4 * grp + r;
+          const int lo = __shfl((int)(kslot & 0xFFFFFFFF), src);
+          const int hi = __shfl((int)(kslot >> 32), src);
+          const int64_t vs = ((int64_t)hi << 32) | (uint32_t)lo;
+          const bool on = vs >= 0;
+          vr[r] = on ? load_kv16v(vbase + vs * a.kv_ss + 8 * col) : z;
+          ok |= (unsigned)on << r;
+        }
+      }
+      return ok;
+    };
+
+    float m_run = -INFINITY;  // running max of head column col (same in all 4 rows)
+    float l_run = 0.f;        // this row's share of the running sum
+    float acc[GPW][8];
+#pragma unroll
+    for (int g = 0; g < GPW; ++g)
+#pragma unroll
+      for (int d = 0; d < 8; ++d) acc[g][d] = 0.f;
+
+    auto tile = [&](const u32x4* kr, const u32x4* vr, unsigned ok) {
+      f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int m = 0; m < 4; ++m) s = MMA::mma(kr[m], qb[m], s);
+      float p[4];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        p[r] = ((ok >> r) & 1u) ? s[r] * a.scale_log2 : -INFINITY;
+        mx = fmaxf(mx, p[r]);
+      }
+      mx = rows_max(mx);
+      const float mn = fmaxf(m_run, mx);
+      const float mref = mn == -INFINITY ? 0.f : mn;  // all masked so far: stay at 0
+      const float alpha = __builtin_amdgcn_exp2f(m_run - mref);
+      m_run = mn;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) p[r] = __builtin_amdgcn_exp2f(p[r] - mref);
+      l_run = __builtin_fmaf(l_run, alpha, (p[0] + p[1]) + (p[2] + p[3]));
+      float vf[4][8];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) unpack16v<DT>(vr[r], vf[r]);
+#pragma unroll
+      for (int g = 0; g < GPW; ++g) {
+        const float al = row_bcast(alpha, g);
+#pragma unroll
+        for (int d = 0; d < 8; ++d) acc[g][d] *= al;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float pr = row_bcast(p[r], g);
+#pragma unroll
+          for (int d = 0; d < 8; ++d) acc[g][d] = __builtin_fmaf(pr, vf[r][d], acc[g][d]);
+        }
+      }
+    };
+
+    if (t0 < t1) {
+      load_table(block_of(t0));
+#if PKV_DECODE_PREFETCH >= 2
+      // Three tile buffers in rotation: two tiles in flight while one is reduced.
+      u32x4 k0[4], v0[4], k1[4], v1[4], k2[4], v2[4];
+      unsigned ok0 = load_tile(t0, k0, v0);
+      unsigned ok1 = load_tile(t0 + TILE, k1, v1);
+      unsigned ok2;
+      for (int tb = t0; tb < t1; tb += 3 * TILE) {
+        ok2 = load_tile(tb + 2 * TILE, k2, v2);
+        tile(k0, v0, ok0);
+        if (tb + TILE >= t1) break;
+        ok0 = load_tile(tb + 3 * TILE, k0, v0);
+        tile(k1, v1, ok1);
+        if (tb + 2 * TILE >= t1) break;
+        ok1 = load_tile(tb + 4 * TILE, k1, v1);
+        tile(k2, v2, ok2);
+      }
+#else
+      // Two tile buffers in ping-pong: the next tile is in flight while one is reduced.
+      u32x4 ka[4], va[4], kb2[4], vb2[4];
+      unsigned oka = load_tile(t0, ka, va);
+      for (int tb = t0; tb < t1; tb += 2 * TILE) {
+        const unsigned okb = load_tile(tb + TILE, kb2, vb2);
+        tile(ka, va, oka);
+        if (tb + TILE >= t1) break;
+        oka = load_tile(tb + 2 * TILE, ka, va);
+        tile(kb2, vb2, okb);
+      }
+#endif
+    }
+
+    // Totals: l over the four rows of each column, acc over the four rows.
+    const float l_tot = rows_sum(l_run);
+#pragma unroll
+    for (int g = 0; g < GPW; ++g)
+#pragma unroll
+      for (int d = 0; d < 8; ++d) acc[g][d] = rows_sum(acc[g][d]);
+    float lh[GPW], mh[GPW];
+#pragma unroll
+    for (int g = 0; g < GPW; ++g) {
+      lh[g] = row_bcast(l_tot, g);
+      mh[g] = row_bcast(m_run, g);
+    }
+
+    if (grp == 0) {  // lane c writes head dims 8c .. 8c + 7
+      const int d0 = 8 * col;
+      if (whole) {
+#pragma unroll
+        for (int g = 0; g < GPW; ++g) {
+          const float inv = lh[g] > 0.f ? 1.f / lh[g] : 0.f;
+          float o[8];
+#pragma unroll
+          for (int d = 0; d < 8; ++d) o[d] = acc[g][d] * inv;
+          const int64_t e = b * a.out_sb + (int64_t)(h0 + g) * a.out_sh + d0;
+          if (a.out_f32) store_vec<PKV_F32, 8>((float*)a.out + e, o);
+          else store_vec<DT, 8>((S*)a.out + e, o);
+          if (a.lse && col == 0) a.lse[(int64_t)b * a.nh + h0 + g] = lse_of(mh[g], lh[g]);
+        }
+      } else {
+#pragma unroll
+        for (int g = 0; g < GPW; ++g) {
+          const int64_t rec = ((int64_t)w * 2 + slot) * a.nh + h0 + g;
+          store_vec<PKV_F32, 8>(a.ws_acc + rec * HD + d0, acc[g]);
+          if (col == 0) *reinterpret_cast<float2*>(a.ws_ml + 2 * rec) = make_float2(mh[g], lh[g]);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// Combine pass: merges the pieces of sequences cut by a range boundary.
+//
+// Sequence b (units [ub, ue)) spans workgroups w0..w1; each non-empty range among them
+// holds one piece and wrote one record per query head (in w0 it is the range's last
+// piece, slot 1, unless the range starts with it). One wave per (sequence, query head)
+// merges them: out = sum_j w_j acc_j / sum_j w_j l_j with w_j = exp2(m_j - max m). The
+// sequence's merge plan (16 bytes written by the stream pass) says which records to
+// read; then one round trip per 4 records loads their (m, l) pairs and accumulator
+// rows together (4 keeps the kernel near 64 VGPRs, so a whole batch's waves are
+// resident at once). Cascade prefix parts are folded in after the records. Sequences
+// that were not cut exit after reading the plan: the stream pass finished them.
+// ---------------------------------------------------------------------------------
+
+// Total units, and the unit range [ub, ue) of sequence b, in one pass over the lengths.
+__device__ void seq_units(const DecodeArgs& a, int b, int64_t* ub, int64_t* ue, int64_t* total) {
+  const int lane = threadIdx.x & (kWave - 1);
+  int64_t before = 0, all = 0;
+  int mine = 0;
+  for (int c0 = 0; c0 < a.batch; c0 += kWave) {
+    const int bb = c0 + lane;
+    const int cnt = bb < a.batch ? units_of(a, clamped_ctx(a, bb)) : 0;
+    int lt = bb < b ? cnt : 0;
+    int tot = cnt;
+    if (bb == b) mine = cnt;
+#pragma unroll
+    for (int s = 1; s < kWave; s <<= 1) {
+      lt += __shfl_xor(lt, s);
+      tot += __shfl_xor(tot, s);
+    }
+    before += lt;
+    all += tot;
+  }
+#pragma unroll
+  for (int s = 1; s < kWave; s <<= 1) mine += __shfl_xor(mine, s);
+  *ub = before;
+  *ue = before + mine;
+  *total = all;
+}
+
+template <int DT, int HD>
+__global__ void __launch_bounds__(256)
+paged_decode_combine_kernel(const DecodeArgs a) {
+  constexpr int DPL = HD >= kWave ? HD / kWave : 1;  // head dims per lane
+  constexpr int kChunk = 4;                           // records loaded per round trip
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wid = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  if (wid >= a.batch * a.nh) return;  // uniform per wave
+  const int b = wid / a.nh, h = wid - b * a.nh;
+
+  const int4 plan = a.desc[b];
+  const int nrec = plan.y;
+  const bool cascade = a.pre_row != nullptr;
+  if (nrec <= 1 && !cascade) return;  // written directly by the stream pass
+  const int64_t w0 = plan.x;
+  // Units fewer than workgroups leave some ranges empty: then find the live ones.
+  int64_t ub = 0, ue = 0, total = 0;
+  if (!plan.w) seq_units(a, b, &ub, &ue, &total);
+  const int64_t row0 = (w0 * 2 + plan.z) * a.nh + h;  // record 0: always live
+
+  float out_acc[DPL], lsum = 0.f, mmax = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < DPL; ++k) out_acc[k] = 0.f;
+  // Fold records [j0, j0 + C) into the running (max, sum, acc). Every load is issued
+  // before any is used. Dead slots (past the last record, or an empty range) re-read
+  // record 0 -- finite data -- and get weight 0: records that were never written are
+  // not read, the scratch may hold NaN bit patterns.
+  // Liveness of records j0 .. j0 + 63, one per lane (a range can be empty only when
+  // units < workgroups; the test divides, so it is done once per lane, not per record).
+  uint64_t live_bits = 0;
+  auto live_block = [&](int j0) {
+    const int j = j0 + lane;
+    bool live = j < nrec;
+    if (!plan.w && live) {
+      const int64_t ww = w0 + j;
+      live = range_start(ww, total, a.num_wg) < range_start(ww + 1, total, a.num_wg);
+    }
+    live_bits = __ballot(live);
+  };
+  auto fold = [&](auto chunk, int j0) {
+    constexpr int C = decltype(chunk)::value;
+    float m[C], l[C], x[C][DPL];
+#pragma unroll
+    for (int jj = 0; jj < C; ++jj) {
+      const int j = j0 + jj;
+      const bool live = (live_bits >> (j & (kWave - 1))) & 1;
+      const int64_t row = (live && j > 0) ? (w0 + j) * 2 * a.nh + h : row0;
+      const float2 ml = *reinterpret_cast<const float2*>(a.ws_ml + 2 * row);
+      m[jj] = live ? ml.x : -INFINITY;
+      l[jj] = ml.y;
+      const float* rowp = a.ws_acc + row * HD;
+#pragma unroll
+      for (int k = 0; k < DPL; ++k) x[jj][k] = (lane + kWave * k < HD) ? rowp[lane + kWave * k] : 0.f;
+    }
+    float mn = mmax;
+#pragma unroll
+    for (int jj = 0; jj < C; ++jj) mn = fmaxf(mn, m[jj]);
+    const float mref = mn == -INFINITY ? 0.f : mn;  // no live token yet: weights 0
+    const float alpha = __builtin_amdgcn_exp2f(mmax - mref);
+    mmax = mn;
+    lsum *= alpha;
+#pragma unroll
+    for (int k = 0; k < DPL; ++k) out_acc[k] *= alpha;
+#pragma unroll
+    for (int jj = 0; jj < C; ++jj) {
+      const float wj = __builtin_amdgcn_exp2f(m[jj] - mref);  // dead: exp2(-inf) = 0
+      lsum = __builtin_fmaf(wj, l[jj], lsum);
+#pragma unroll
+      for (int k = 0; k < DPL; ++k) out_acc[k] = __builtin_fmaf(wj, x[jj][k], out_acc[k]);
+    }
+  };
+  if (nrec <= 1) {
+    // Cascade, finished by the stream pass: its normalised fp32 output and log2
+    // normaliser are the state (lse, 1, O); an empty context (-inf) weighs nothing.
+    const float lt = a.lse[(int64_t)b * a.nh + h];
+    mmax = lt;
+    lsum = lt == -INFINITY ? 0.f : 1.f;
+    const float* t = reinterpret_cast<const float*>(a.out) + b * a.out_sb + (int64_t)h * a.out_sh;
+#pragma unroll
+    for (int k = 0; k < DPL; ++k) out_acc[k] = (lane + kWave * k < HD) ? t[lane + kWave * k] : 0.f;
+  } else {
+    for (int j0 = 0; j0 < nrec; j0 += kChunk) {
+      if ((j0 & (kWave - 1)) == 0) live_block(j0);
+      fold(std::integral_constant<int, kChunk>{}, j0);
+    }
+  }
+  if (cascade) fold_prefix<HD, DPL>(a, b, h, mmax, lsum, out_acc);
+  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+  float* lse_dst = cascade ? a.fin_lse : a.lse;
+  if (lse_dst && lane == 0) lse_dst[(int64_t)b * a.nh + h] = lse_of(mmax, lsum);
+  void* dst = cascade ? a.fin : a.out;
+  const int64_t sb = cascade ? a.fin_sb : a.out_sb, sh = cascade ? a.fin_sh : a.out_sh;
+  const bool f32 = cascade ? a.fin_f32 : a.out_f32;
+#pragma unroll
+  for (int k = 0; k < DPL; ++k) {
+    const int d = lane + kWave * k;
+    if (d >= HD) break;
+    const float o = out_acc[k] * inv;
+    const int64_t e = b * sb + (int64_t)h * sh + d;
+    if (f32) reinterpret_cast<float*>(dst)[e] = o;
+    else reinterpret_cast<typename Elt<DT>::S*>(dst)[e] = Elt<DT>::from_f32(o);
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// Host-side dispatch.
+// ---------------------------------------------------------------------------------
+
+// Decode scratch, byte offsets of its areas (each 256-byte aligned): the merge plans
+// [batch] int4 (split or cascade), the partial records [num_wg, 2, nh, hd] fp32 and
+// their (max, sum) pairs (split: num_wg > 1), and the finished-sequence outputs
+// [batch, nh, hd] fp32 with their normalisers [batch, nh] (cascade). total = 0: no
+// scratch needed.
+struct DecodeWs {
+  int64_t desc = -1, acc = -1, ml = -1, tail_o = -1, tail_lse = -1, total = 0;
+};
+DecodeWs decode_ws(int32_t num_wg, int32_t batch, int32_t nh, int32_t hd, bool cascade) {
+  DecodeWs w;
+  const bool split = num_wg > 1;
+  if (batch <= 0 || nh <= 0 || hd <= 0 || !(split || cascade)) return w;
+  int64_t at = 0;
+  auto place = [&](int64_t bytes) {
+    const int64_t off = (at + 255) / 256 * 256;
+    at = off + bytes;
+    return off;
+  };
+  w.desc = place((int64_t)batch * 16);
+  if (split) {
+    const int64_t recs = (int64_t)num_wg * 2 * nh;
+    w.acc = place(recs * hd * 4);
+    w.ml = place(recs * 2 * 4);
+  }
+  if (cascade) {
+    w.tail_o = place((int64_t)batch * nh * hd * 4);
+    w.tail_lse = place((int64_t)batch * nh * 4);
+  }
+  w.total = at;
+  return w;
+}
+
+// Run f.run<DT, HD, GPW>() for the runtime (dtype, head_dim, heads per wave).
+template <int DT, int HD, class F> hipError_t by_gpw(int gpw, const F& f) {
+  switch (gpw) {
+    case 1: return f.template run<DT, HD, 1>();
+    case 2: return f.template run<DT, HD, 2>();
+    case 3: return f.template run<DT, HD, 3>();
+    default: return f.template run<DT, HD, 4>();
+  }
+}
+template <int DT, class F> hipError_t by_hd(int hd, int gpw, const F& f) {
+  switch (hd) {
+    case 16: return by_gpw<DT, 16>(gpw, f);
+    case 32: return by_gpw<DT, 32>(gpw, f);
+    case 64: return by_gpw<DT, 64>(gpw, f);
+    case 128: return by_gpw<DT, 128>(gpw, f);
+    default: return by_gpw<DT, 256>(gpw, f);
+  }
+}
+template <class F> hipError_t by_dtype(int dt, int hd, int gpw, const F& f) {
+  switch (dt) {
+    case PKV_F32: return by_hd<PKV_F32>(hd, gpw, f);
+    case PKV_F16: return by_hd<PKV_F16>(hd, gpw, f);
+    default: return by_hd<PKV_BF16>(hd, gpw, f);
+  }
+}
+
+// The MFMA kernel serves 16-bit K/V at head_dim 128; every other shape uses the
+// generic stream kernel.
+template <int DT, int HD> constexpr bool use_mfma() {
+  return DT != PKV_F32 && HD == 128 && PKV_DECODE_USE_MFMA;
+}
+template <int DT, int HD, int GPW> const void* decode_kernel() {
+  if constexpr (use_mfma<DT, HD>())
+    return reinterpret_cast<const void*>(&paged_decode_mfma_kernel<DT, GPW, true>);
+  else
+    return reinterpret_cast<const void*>(&paged_decode_stream_kernel<DT, HD, GPW>);
+}
+
+struct LaunchDecode {
+  const DecodeArgs* a;
+  int wpg, ygrid;
+  hipStream_t st;
+  template <int DT, int HD, int GPW> hipError_t run() const {
+    const dim3 grid((unsigned)a->num_wg, (unsigned)ygrid), block(kWave * wpg);
+    if constexpr (use_mfma<DT, HD>()) {
+      if (a->bs % 16 == 0)
+        hipLaunchKernelGGL((paged_decode_mfma_kernel<DT, GPW, true>), grid, block, 0, st, *a);
+      else
+        hipLaunchKernelGGL((paged_decode_mfma_kernel<DT, GPW, false>), grid, block, 0, st, *a);
+    } else {
+      hipLaunchKernelGGL((paged_decode_stream_kernel<DT, HD, GPW>), grid, block, 0, st, *a);
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || (a->num_wg <= 1 && !a->pre_row)) return e;
+    const int waves = a->batch * a->nh;
+    hipLaunchKernelGGL((paged_decode_combine_kernel<DT, HD>), dim3((unsigned)((waves + 3) / 4)),
+                       dim3(256), 0, st, *a);
+    return hipGetLastError();
+  }
+};
+
+// Unit size (TILE tokens) of an instantiation, and how many of its workgroups one CU
+// holds at once.
+struct QueryDecode {
+  int wpg;
+  int* tile;
+  int* per_cu;  // may be null: tile only
+  template <int DT, int HD, int GPW> hipError_t run() const {
+    *tile = DecodeShape<DT, HD>::TILE;
+    if (!per_cu) return hipSuccess;
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, decode_kernel<DT, HD, GPW>(),
+                                                         kWave * wpg, 0);
+  }
+};
+
+// Query heads per wave: the whole group when it has at most 4 heads (the register
+// budget of 4 heads x 8 fp32 accumulators keeps the kernel spill-free at hd 256), else
+// the largest of {4, 3, 2} that divides the group, else 1. Waves that share a KV head
+// read the same rows within a few hundred cycles of each other, so the repeat is served
+// from L2, not HBM.
+int pick_gpw(int groups) {
+  if (groups <= 4) return groups;
+  const int cands[3] = {4, 3, 2};
+  for (int c : cands)
+    if (groups % c == 0) return c;
+  return 1;
+}
+
+// Waves per workgroup and workgroups along y for num_kv_heads x (groups / gpw) tasks.
+struct DecodePlan {
+  int gpw, nsub, wpg, ygrid;
+};
+DecodePlan plan_decode(int num_heads, int num_kv_heads) {
+  DecodePlan p;
+  const int groups = num_heads / num_kv_heads;
+  p.gpw = pick_gpw(groups);
+  p.nsub = groups / p.gpw;
+  const int tasks = num_kv_heads * p.nsub;
+  p.wpg = tasks < PKV_DECODE_WAVES_PER_WG ? tasks : PKV_DECODE_WAVES_PER_WG;
+  p.ygrid = (tasks + p.wpg - 1) / p.wpg;
+  return p;
+}
+
+int check_decode_shape(int kv_dtype, int head_dim, int num_heads, int num_kv_heads) {
+  if (!valid_dtype(kv_dtype)) return PKV_E_DTYPE;
+  if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0) return PKV_E_SHAPE;
+  if (!(head_dim == 16 || head_dim == 32 || head_dim == 64 || head_dim == 128 ||
+        head_dim == 256))
+    return PKV_E_SHAPE;
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t pkv_decode_workgroups(int kv_dtype, int32_t head_dim, int32_t num_heads,
+                              int32_t num_kv_heads) {
+  const int bad = check_decode_shape(kv_dtype, head_dim, num_heads, num_kv_heads);
+  if (bad) return bad;
+  const DecodePlan p = plan_decode(num_heads, num_kv_heads);
+  int dev = 0, cus = 0, per_cu = 0, tile = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e == hipSuccess) e = by_dtype(kv_dtype, head_dim, p.gpw, QueryDecode{p.wpg, &tile, &per_cu});
+  if (e != hipSuccess) return PKV_E_HIP;
+  const int g = cus * (per_cu < 1 ? 1 : per_cu) / p.ygrid;
+  return g < 1 ? 1 : g;
+}
+
+int64_t pkv_decode_workspace_bytes(int32_t num_workgroups, int32_t batch, int32_t num_heads,
+                                   int32_t head_dim) {
+  return decode_ws(num_workgroups, batch, num_heads, head_dim, false).total;
+}
+
+int64_t pkv_cascade_workspace_bytes(int32_t num_workgroups, int32_t batch, int32_t num_heads,
+                                    int32_t head_dim) {
+  return decode_ws(num_workgroups, batch, num_heads, head_dim, true).total;
+}
+
+int pkv_paged_decode(void* out, int out_dtype, int64_t out_stride_b, int64_t out_stride_h,
+                     const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                     const void* k_cache, const void* v_cache, int kv_dtype,
+                     int64_t kv_stride_slot, int64_t kv_stride_head, int64_t num_slots,
+                     const int32_t* block_tables, int64_t table_stride, int32_t max_blocks,
+                     const int32_t* context_lens, int32_t batch, int32_t num_heads,
+                     int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                     float scale, int32_t num_workgroups, void* workspace,
+                     int64_t workspace_bytes, void* stream) {
+  return pkv_paged_decode_ex(out, out_dtype, out_stride_b, out_stride_h, q, q_stride_b,
+                             q_stride_h, k_cache, v_cache, kv_dtype, kv_stride_slot,
+                             kv_stride_head, num_slots, block_tables, table_stride, max_blocks,
+                             context_lens, batch, num_heads, num_kv_heads, head_dim, block_size,
+                             scale, num_workgroups, workspace, workspace_bytes, nullptr,
+                             nullptr, nullptr, nullptr, nullptr, 0, 0, stream);
+}
+
+int pkv_paged_decode_ex(void* out, int out_dtype, int64_t out_stride_b, int64_t out_stride_h,
+                        const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                        const void* k_cache, const void* v_cache, int kv_dtype,
+                        int64_t kv_stride_slot, int64_t kv_stride_head, int64_t num_slots,
+                        const int32_t* block_tables, int64_t table_stride, int32_t max_blocks,
+                        const int32_t* context_lens, int32_t batch, int32_t num_heads,
+                        int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                        float scale, int32_t num_workgroups, void* workspace,
+                        int64_t workspace_bytes, const int32_t* first_block, float* lse,
+                        const float* prefix_out, const float* prefix_lse,
+                        const int32_t* prefix_row, int32_t prefix_parts,
+                        int64_t prefix_stride, void* stream) {
+  const int bad = check_decode_shape(kv_dtype, head_dim, num_heads, num_kv_heads);
+  if (bad) return bad;
+  const bool cascade = prefix_row != nullptr && prefix_parts > 0;
+  if (prefix_parts < 0 || prefix_stride < 0) return PKV_E_SHAPE;
+  if (cascade && (!prefix_out || !prefix_lse)) return PKV_E_NULL;
+  if (cascade && !aligned16(prefix_out)) return PKV_E_ALIGN;
+  if (!(out_dtype == kv_dtype || out_dtype == PKV_F32)) return PKV_E_DTYPE;
+  if (batch < 0 || block_size <= 0 || max_blocks < 0 || num_workgroups < 1 ||
+      num_workgroups > (1 << 24) || batch > (1 << 24))
+    return PKV_E_SHAPE;
+  if ((int64_t)max_blocks * block_size > (int64_t)1 << 30) return PKV_E_SHAPE;
+  if (batch == 0) return 0;
+  if (!out || !q || !k_cache || !v_cache || !context_lens || (max_blocks > 0 && !block_tables))
+    return PKV_E_NULL;
+  const int vec = kv_dtype == PKV_F32 ? 4 : 8;
+  if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out) ||
+      q_stride_b % vec || q_stride_h % vec || kv_stride_slot % vec || kv_stride_head % vec ||
+      out_stride_b % vec || out_stride_h % vec)
+    return PKV_E_ALIGN;
+  const DecodePlan p = plan_decode(num_heads, num_kv_heads);
+
+  DecodeArgs a;
+  a.out = out;
+  a.out_sb = out_stride_b;
+  a.out_sh = out_stride_h;
+  a.q = q;
+  a.q_sb = q_stride_b;
+  a.q_sh = q_stride_h;
+  a.k = k_cache;
+  a.v = v_cache;
+  a.kv_ss = kv_stride_slot;
+  a.kv_sh = kv_stride_head;
+  a.num_slots = num_slots;
+  a.tables = block_tables;
+  a.table_stride = table_stride;
+  a.max_blocks = max_blocks;
+  a.ctx = context_lens;
+  a.batch = batch;
+  a.nh = num_heads;
+  a.nkv = num_kv_heads;
+  a.groups = num_heads / num_kv_heads;
+  a.nsub = p.nsub;
+  a.bs = block_size;
+  a.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz(block_size) : -1;
+  int tile = 0;
+  (void)by_dtype(kv_dtype, head_dim, p.gpw, QueryDecode{p.wpg, &tile, nullptr});
+  a.unit_tokens = tile;
+  a.num_wg = num_workgroups;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  a.out_f32 = out_dtype == PKV_F32;
+  a.first_block = first_block;
+  a.lse = lse;
+  a.pre_o = cascade ? prefix_out : nullptr;
+  a.pre_lse = cascade ? prefix_lse : nullptr;
+  a.pre_row = cascade ? prefix_row : nullptr;
+  a.pre_parts = cascade ? prefix_parts : 0;
+  a.pre_stride = prefix_stride;
+  a.fin = nullptr;
+  a.fin_lse = nullptr;
+  a.fin_sb = a.fin_sh = 0;
+  a.fin_f32 = 0;
+  a.desc = nullptr;
+  a.ws_acc = nullptr;
+  a.ws_ml = nullptr;
+  const DecodeWs ws = decode_ws(num_workgroups, batch, num_heads, head_dim, cascade);
+  if (ws.total) {
+    if (!workspace || workspace_bytes < ws.total || !aligned16(workspace)) return PKV_E_WORKSPACE;
+    char* base = (char*)workspace;
+    a.desc = (int4*)(base + ws.desc);
+    if (ws.acc >= 0) {
+      a.ws_acc = (float*)(base + ws.acc);
+      a.ws_ml = (float*)(base + ws.ml);
+    }
+    if (cascade) {  // the stream pass finishes sequences into fp32 scratch; combine merges
+      a.fin = out;
+      a.fin_sb = out_stride_b;
+      a.fin_sh = out_stride_h;
+      a.fin_f32 = a.out_f32;
+      a.fin_lse = lse;
+      a.out = base + ws.tail_o;
+      a.out_sb = (int64_t)num_heads * head_dim;
+      a.out_sh = head_dim;
+      a.out_f32 = 1;
+      a.lse = (float*)(base + ws.tail_lse);
+    }
+  }
+
+  hipStream_t st = (hipStream_t)stream;
+  return (int)by_dtype(kv_dtype, head_dim, p.gpw, LaunchDecode{&a, p.wpg, p.ygrid, st});
+}
+
+}  // extern "C"
