@@ -101,33 +101,39 @@ __device__ __forceinline__ float lse_of(float m, float l) {
   return l > 0.f ? m + __log2f(l) : -INFINITY;
 }
 
-// Folds sequence b's prefix parts for head h into a wave's running softmax state (m, l,
-// acc), lane holding head dims lane + 64 c (c < DPL; dims >= HD skipped). A part is a
-// normalised output O_k with log2 normaliser lse_k, i.e. the state (lse_k, 1, O_k):
-// with M the new max, l <- l 2^(m - M) + sum_k 2^(lse_k - M) and likewise acc. Parts
-// are loaded eight at a time, every load issued before any is used.
-template <int HD, int DPL>
-__device__ __forceinline__ void fold_prefix(const DecodeArgs& a, int b, int h, float& m,
-                                            float& l, float (&acc)[DPL]) {
-  const int r = a.pre_row[b];
-  if (r < 0) return;
-  const int lane = threadIdx.x & (kWave - 1);
-  constexpr int C = 8;
-  for (int k0 = 0; k0 < a.pre_parts; k0 += C) {
-    float lk[C], x[C][DPL];
+// A sequence's cascade prefix parts for head h, eight at a time. Part k is a normalised
+// output O_k (row pre + k * pre_stride of pre_o) with log2 normaliser lse_k, i.e. the
+// softmax state (lse_k, 1, O_k); folding it into a wave's running state (m, l, acc)
+// (lane holding head dims lane + 64 c, c < DPL) is, with M the new max,
+// l <- l 2^(m - M) + sum_k 2^(lse_k - M) and likewise acc. load() issues a chunk's loads
+// (lane j < 8 fetches part k0 + j's normaliser, one vector load for the chunk), fold()
+// consumes them, so the first chunk can be in flight while the records are merged.
+template <int HD, int DPL> struct PrefixParts {
+  static constexpr int C = 8;
+  float lk;         // lane j: lse of part k0 + (j mod 8), -inf past the last part
+  float x[C][DPL];  // the chunk's output rows
+
+  __device__ __forceinline__ static int64_t row(const DecodeArgs& a, int pre, int h, int k) {
+    return ((int64_t)pre + (int64_t)(k < a.pre_parts ? k : 0) * a.pre_stride) * a.nh + h;
+  }
+  __device__ __forceinline__ void load(const DecodeArgs& a, int pre, int h, int k0) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int kl = k0 + (lane & (C - 1));
+    lk = kl < a.pre_parts ? a.pre_lse[row(a, pre, h, kl)] : -INFINITY;
 #pragma unroll
-    for (int jj = 0; jj < C; ++jj) {
-      const int k = k0 + jj;
-      const bool live = k < a.pre_parts;
-      const int64_t row = ((int64_t)r + (int64_t)(live ? k : 0) * a.pre_stride) * a.nh + h;
-      lk[jj] = live ? a.pre_lse[row] : -INFINITY;
-      const float* p = a.pre_o + row * HD;
+    for (int j = 0; j < C; ++j) {
+      const float* p = a.pre_o + row(a, pre, h, k0 + j) * HD;
 #pragma unroll
-      for (int c = 0; c < DPL; ++c) x[jj][c] = lane + kWave * c < HD ? p[lane + kWave * c] : 0.f;
+      for (int c = 0; c < DPL; ++c) x[j][c] = lane + kWave * c < HD ? p[lane + kWave * c] : 0.f;
     }
+  }
+  __device__ __forceinline__ void fold(float& m, float& l, float (&acc)[DPL]) const {
+    float lj[C];
+#pragma unroll
+    for (int j = 0; j < C; ++j) lj[j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lk), j));
     float mn = m;
 #pragma unroll
-    for (int jj = 0; jj < C; ++jj) mn = fmaxf(mn, lk[jj]);
+    for (int j = 0; j < C; ++j) mn = fmaxf(mn, lj[j]);
     const float mref = mn == -INFINITY ? 0.f : mn;  // nothing live yet: weights 0
     const float alpha = __builtin_amdgcn_exp2f(m - mref);
     m = mn;
@@ -135,14 +141,14 @@ __device__ __forceinline__ void fold_prefix(const DecodeArgs& a, int b, int h, f
 #pragma unroll
     for (int c = 0; c < DPL; ++c) acc[c] *= alpha;
 #pragma unroll
-    for (int jj = 0; jj < C; ++jj) {
-      const float wj = __builtin_amdgcn_exp2f(lk[jj] - mref);  // dead or empty: 0
+    for (int j = 0; j < C; ++j) {
+      const float wj = __builtin_amdgcn_exp2f(lj[j] - mref);  // dead or empty: 0
       l += wj;
 #pragma unroll
-      for (int c = 0; c < DPL; ++c) acc[c] = __builtin_fmaf(wj, x[jj][c], acc[c]);
+      for (int c = 0; c < DPL; ++c) acc[c] = __builtin_fmaf(wj, x[j][c], acc[c]);
     }
   }
-}
+};
 
 __device__ __forceinline__ int units_of(const DecodeArgs& a, int n) {
   return n == 0 ? 1 : (n + a.unit_tokens - 1) / a.unit_tokens;
@@ -179,6 +185,37 @@ __device__ int find_unit(const DecodeArgs& a, int64_t target, int64_t* ustart) {
 __device__ __forceinline__ int64_t range_start(int64_t w, int64_t units, int64_t wgs) {
   return w * units / wgs;
 }
+
+// Workgroup w's unit range [*rs, *re) and the sequence b owning unit *rs (first unit
+// *ub); returns batch when the range is empty. A batch that fits one wave is scanned
+// once (the lengths' prefix sums give both the total and the owner); larger batches
+// take two passes of find_unit. Call from whole waves.
+__device__ int locate_range(const DecodeArgs& a, int w, int64_t* total, int64_t* rs,
+                            int64_t* re, int64_t* ub) {
+  if (a.batch <= kWave) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int cnt = lane < a.batch ? units_of(a, clamped_ctx(a, lane)) : 0;
+    int incl = cnt;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const int t = __shfl_up(incl, off);
+      if (lane >= off) incl += t;
+    }
+    *total = __shfl(incl, kWave - 1);
+    *rs = range_start(w, *total, a.num_wg);
+    *re = range_start(w + 1, *total, a.num_wg);
+    if (*rs >= *re) return a.batch;
+    const unsigned long long hit = __ballot(incl > *rs);
+    const int l = __ffsll((long long)hit) - 1;
+    *ub = __shfl(incl - cnt, l);
+    return l;
+  }
+  find_unit(a, -1, total);
+  *rs = range_start(w, *total, a.num_wg);
+  *re = range_start(w + 1, *total, a.num_wg);
+  if (*rs >= *re) return a.batch;
+  return find_unit(a, *rs, ub);
+}
 // The workgroup whose range holds unit u: the largest w with range_start(w) <= u.
 __device__ __forceinline__ int64_t wg_of_unit(int64_t u, int64_t units, int64_t wgs) {
   return ((u + 1) * wgs - 1) / units;
@@ -210,13 +247,9 @@ paged_decode_stream_kernel(const DecodeArgs a) {
   const int h0 = kvh * a.groups + (task - kvh * a.nsub) * GPW;
   const int w = blockIdx.x;
 
-  int64_t total;
-  find_unit(a, -1, &total);
-  const int64_t rs = range_start(w, total, a.num_wg);
-  const int64_t re = range_start(w + 1, total, a.num_wg);
+  int64_t total, rs, re, ub;
+  int b = locate_range(a, w, &total, &rs, &re, &ub);
   if (rs >= re) return;
-  int64_t ub;
-  int b = find_unit(a, rs, &ub);
 
   const int row = lane / LPT;         // token sub-index inside a load
   const int d0 = (lane % LPT) * VEC;  // this lane's first head_dim element
@@ -456,13 +489,9 @@ paged_decode_mfma_kernel(const DecodeArgs a) {
   const int h0 = kvh * a.groups + (task - kvh * a.nsub) * GPW;
   const int w = blockIdx.x;
 
-  int64_t total;
-  find_unit(a, -1, &total);
-  const int64_t rs = range_start(w, total, a.num_wg);
-  const int64_t re = range_start(w + 1, total, a.num_wg);
+  int64_t total, rs, re, ub;
+  int b = locate_range(a, w, &total, &rs, &re, &ub);
   if (rs >= re) return;
-  int64_t ub;
-  int b = find_unit(a, rs, &ub);
 
   const int col = lane & 15, grp = lane >> 4;
   // FAST: block_size is a multiple of 16, so a tile never crosses a block.
@@ -694,10 +723,11 @@ paged_decode_mfma_kernel(const DecodeArgs a) {
 // piece, slot 1, unless the range starts with it). One wave per (sequence, query head)
 // merges them: out = sum_j w_j acc_j / sum_j w_j l_j with w_j = exp2(m_j - max m). The
 // sequence's merge plan (16 bytes written by the stream pass) says which records to
-// read; then one round trip per 4 records loads their (m, l) pairs and accumulator
-// rows together (4 keeps the kernel near 64 VGPRs, so a whole batch's waves are
-// resident at once). Cascade prefix parts are folded in after the records. Sequences
-// that were not cut exit after reading the plan: the stream pass finished them.
+// read. Then one round trip loads up to 64 records' (m, l) pairs (one per lane), and
+// the accumulator rows follow in chunks whose loads overlap: a sequence cut into many
+// pieces (a long context) costs about three round trips, not one per few records.
+// Cascade prefix parts are folded in after the records. Sequences that were not cut
+// exit after reading the plan: the stream pass finished them.
 // ---------------------------------------------------------------------------------
 
 // Total units, and the unit range [ub, ue) of sequence b, in one pass over the lengths.
@@ -730,16 +760,22 @@ template <int DT, int HD>
 __global__ void __launch_bounds__(256)
 paged_decode_combine_kernel(const DecodeArgs a) {
   constexpr int DPL = HD >= kWave ? HD / kWave : 1;  // head dims per lane
-  constexpr int kChunk = 4;                           // records loaded per round trip
+  constexpr int kChunk = PKV_DECODE_COMBINE_CHUNK;    // accumulator rows per load batch
   const int lane = threadIdx.x & (kWave - 1);
-  const int wid = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
-  if (wid >= a.batch * a.nh) return;  // uniform per wave
+  // Wave-uniform by construction; readfirstlane lets the compiler keep the plan, record
+  // indices and row bases in scalar registers.
+  const int wid = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave);
+  if (wid >= a.batch * a.nh) return;
   const int b = wid / a.nh, h = wid - b * a.nh;
 
   const int4 plan = a.desc[b];
-  const int nrec = plan.y;
   const bool cascade = a.pre_row != nullptr;
+  const int pre = cascade ? a.pre_row[b] : -1;  // fetched with the plan
+  const int nrec = plan.y;
   if (nrec <= 1 && !cascade) return;  // written directly by the stream pass
+  // The first prefix parts' loads go out before the records are merged.
+  PrefixParts<HD, DPL> parts;
+  if (pre >= 0) parts.load(a, pre, h, 0);
   const int64_t w0 = plan.x;
   // Units fewer than workgroups leave some ranges empty: then find the live ones.
   int64_t ub = 0, ue = 0, total = 0;
@@ -765,38 +801,6 @@ paged_decode_combine_kernel(const DecodeArgs a) {
     }
     live_bits = __ballot(live);
   };
-  auto fold = [&](auto chunk, int j0) {
-    constexpr int C = decltype(chunk)::value;
-    float m[C], l[C], x[C][DPL];
-#pragma unroll
-    for (int jj = 0; jj < C; ++jj) {
-      const int j = j0 + jj;
-      const bool live = (live_bits >> (j & (kWave - 1))) & 1;
-      const int64_t row = (live && j > 0) ? (w0 + j) * 2 * a.nh + h : row0;
-      const float2 ml = *reinterpret_cast<const float2*>(a.ws_ml + 2 * row);
-      m[jj] = live ? ml.x : -INFINITY;
-      l[jj] = ml.y;
-      const float* rowp = a.ws_acc + row * HD;
-#pragma unroll
-      for (int k = 0; k < DPL; ++k) x[jj][k] = (lane + kWave * k < HD) ? rowp[lane + kWave * k] : 0.f;
-    }
-    float mn = mmax;
-#pragma unroll
-    for (int jj = 0; jj < C; ++jj) mn = fmaxf(mn, m[jj]);
-    const float mref = mn == -INFINITY ? 0.f : mn;  // no live token yet: weights 0
-    const float alpha = __builtin_amdgcn_exp2f(mmax - mref);
-    mmax = mn;
-    lsum *= alpha;
-#pragma unroll
-    for (int k = 0; k < DPL; ++k) out_acc[k] *= alpha;
-#pragma unroll
-    for (int jj = 0; jj < C; ++jj) {
-      const float wj = __builtin_amdgcn_exp2f(m[jj] - mref);  // dead: exp2(-inf) = 0
-      lsum = __builtin_fmaf(wj, l[jj], lsum);
-#pragma unroll
-      for (int k = 0; k < DPL; ++k) out_acc[k] = __builtin_fmaf(wj, x[jj][k], out_acc[k]);
-    }
-  };
   if (nrec <= 1) {
     // Cascade, finished by the stream pass: its normalised fp32 output and log2
     // normaliser are the state (lse, 1, O); an empty context (-inf) weighs nothing.
@@ -807,12 +811,64 @@ paged_decode_combine_kernel(const DecodeArgs a) {
 #pragma unroll
     for (int k = 0; k < DPL; ++k) out_acc[k] = (lane + kWave * k < HD) ? t[lane + kWave * k] : 0.f;
   } else {
-    for (int j0 = 0; j0 < nrec; j0 += kChunk) {
-      if ((j0 & (kWave - 1)) == 0) live_block(j0);
-      fold(std::integral_constant<int, kChunk>{}, j0);
+    // Records in blocks of up to 64: lane r of a block loads record j0 + r's (m, l), one
+    // wave reduction gives the block's max M, and with every weight 2^(m - M) known up
+    // front the accumulator rows stream in chunks of kChunk records, each chunk's loads
+    // issued before the previous chunk is consumed (no round trip waits on another).
+    for (int j0 = 0; j0 < nrec; j0 += kWave) {
+      live_block(j0);
+      const int n = min(kWave, nrec - j0);
+      auto row_of = [&](int r) -> int64_t {  // r < n: record j0 + r, else record 0
+        const bool lv = r < n && ((live_bits >> r) & 1);
+        return (lv && j0 + r > 0) ? (w0 + j0 + r) * 2 * a.nh + h : row0;
+      };
+      float xa[kChunk][DPL], xb[kChunk][DPL];
+      auto load_rows = [&](float (&x)[kChunk][DPL], int c) {
+#pragma unroll
+        for (int jj = 0; jj < kChunk; ++jj) {
+          const float* rowp = a.ws_acc + row_of(c + jj) * HD;
+#pragma unroll
+          for (int k = 0; k < DPL; ++k) x[jj][k] = (lane + kWave * k < HD) ? rowp[lane + kWave * k] : 0.f;
+        }
+      };
+      // The first rows go out with the (m, l) pairs: addresses do not need the weights.
+      const float2 ml = *reinterpret_cast<const float2*>(a.ws_ml + 2 * row_of(lane));
+      load_rows(xa, 0);
+      const bool mine = lane < n && ((live_bits >> lane) & 1);
+      const float mj = mine ? ml.x : -INFINITY;
+      const float mn = fmaxf(mmax, across_max<1>(mj));
+      const float mref = mn == -INFINITY ? 0.f : mn;  // no live token yet: weights 0
+      const float alpha = __builtin_amdgcn_exp2f(mmax - mref);
+      mmax = mn;
+      const float wj = __builtin_amdgcn_exp2f(mj - mref);  // dead: exp2(-inf) = 0
+      lsum = __builtin_fmaf(lsum, alpha, across_sum<1>(wj * ml.y));
+#pragma unroll
+      for (int k = 0; k < DPL; ++k) out_acc[k] *= alpha;
+      auto consume = [&](const float (&x)[kChunk][DPL], int c) {
+#pragma unroll
+        for (int jj = 0; jj < kChunk; ++jj) {
+          const int r = c + jj;
+          const float w = r < n ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wj), r)) : 0.f;
+#pragma unroll
+          for (int k = 0; k < DPL; ++k) out_acc[k] = __builtin_fmaf(w, x[jj][k], out_acc[k]);
+        }
+      };
+      for (int c = 0; c < n; c += 2 * kChunk) {
+        if (c + kChunk < n) load_rows(xb, c + kChunk);
+        consume(xa, c);
+        if (c + kChunk >= n) break;
+        if (c + 2 * kChunk < n) load_rows(xa, c + 2 * kChunk);
+        consume(xb, c + kChunk);
+      }
     }
   }
-  if (cascade) fold_prefix<HD, DPL>(a, b, h, mmax, lsum, out_acc);
+  if (pre >= 0) {
+    parts.fold(mmax, lsum, out_acc);
+    for (int k0 = PrefixParts<HD, DPL>::C; k0 < a.pre_parts; k0 += PrefixParts<HD, DPL>::C) {
+      parts.load(a, pre, h, k0);
+      parts.fold(mmax, lsum, out_acc);
+    }
+  }
   const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
   float* lse_dst = cascade ? a.fin_lse : a.lse;
   if (lse_dst && lane == 0) lse_dst[(int64_t)b * a.nh + h] = lse_of(mmax, lsum);
