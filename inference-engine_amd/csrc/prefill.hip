@@ -216,11 +216,14 @@ paged_prefill_kernel(const PrefillArgs a) {
   const int kvh = item % a.nkv;
   const int rbi = (item / a.nkv) % a.row_blocks;
   const int crank = item / (a.nkv * a.row_blocks);
-  // Each wave ranks up to 64 chunks by itself; larger batches keep their order.
-  int c = crank;
-  if (a.n_chunks <= kWave) {
-    const int cap0 = a.max_blocks * a.bs;
-    const int mine = lane < a.n_chunks ? min(max(a.ctx[lane], 0), cap0) : -1;
+  // Each wave ranks up to 63 chunks by itself; larger batches keep their order. Lane j
+  // fetches chunk j's length and query offset (and lane n_chunks the end offset) in one
+  // round trip, so the chunk's numbers come from the lanes, not a second dependent load.
+  const int cap = a.max_blocks * a.bs;
+  int c = crank, q0, q1, n;
+  if (a.n_chunks < kWave) {
+    const int mine = lane < a.n_chunks ? min(max(a.ctx[lane], 0), cap) : -1;
+    const int cq = lane <= a.n_chunks ? a.cu_q[lane] : 0;
     int rank = 0;
     for (int j = 0; j < a.n_chunks; ++j) {
       const int other = __shfl(mine, j);
@@ -228,14 +231,19 @@ paged_prefill_kernel(const PrefillArgs a) {
     }
     const uint64_t hit = __ballot(lane < a.n_chunks && rank == crank);
     c = __builtin_ctzll(hit);
+    q0 = __builtin_amdgcn_readlane(cq, c);
+    q1 = __builtin_amdgcn_readlane(cq, c + 1);  // c + 1 <= n_chunks < 64
+    n = __builtin_amdgcn_readlane(mine, c);
+  } else {
+    q0 = a.cu_q[c];
+    q1 = a.cu_q[c + 1];
+    n = min(max(a.ctx[c], 0), cap);
   }
-  const int q0 = a.cu_q[c], qlen = a.cu_q[c + 1] - q0;
+  const int qlen = q1 - q0;
   const int G = a.groups;
   const int nrows = qlen * G;
   const int rho0 = (a.row_blocks - 1 - rbi) * BM;
   if (qlen <= 0 || rho0 >= nrows) return;  // uniform per workgroup
-  const int cap = a.max_blocks * a.bs;
-  const int n = min(max(a.ctx[c], 0), cap);
   const int base_pos = n - qlen;  // position of query token 0
 
   // This lane's query row in each of its wave's 16-row tiles (B operand column). Both

@@ -161,3 +161,18 @@ def test_prefill_grid_bound_and_empty_chunks():
     got = _run(q, k, v, tables, ctx, cu, 4, 256)
     want = oracle.prefill_attention(q, k, v, tables, cu, ctx, 4, threads=THREADS)
     assert (got - want).abs().max().item() <= ATOL
+
+
+@pytest.mark.parametrize("n_chunks", [63, 64, 70])
+def test_prefill_many_chunks(n_chunks):
+    """Up to 63 chunks one wave ranks them (and reads each chunk's offsets from the
+    lanes); from 64 on they keep their order and every workgroup loads its own chunk's
+    offsets. Both sides of that boundary, ragged lengths and empty chunks included."""
+    _say("prefill many chunks", n_chunks)
+    g = torch.Generator().manual_seed(n_chunks)
+    qs = torch.randint(0, 20, (n_chunks,), generator=g).tolist()
+    spec = [(qn, qn + int(torch.randint(0, 60, (1,), generator=g))) for qn in qs]
+    q, k, v, tables, ctx, cu = _chunks(spec, 8, 2, 64, 16, torch.bfloat16, seed=n_chunks)
+    got = _run(q, k, v, tables, ctx, cu, 16, max(qs))
+    want = oracle.prefill_attention(q, k, v, tables, cu, ctx, 16, threads=THREADS)
+    assert (got - want).abs().max().item() <= ATOL
