@@ -130,3 +130,28 @@ def test_cascade_config3_matches_plain_decode():
     pa.paged_decode_attention(*args, out=casc, prefix_groups=pg)
     torch.cuda.synchronize()
     assert (plain - casc).abs().max().item() <= 1e-3
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("wgs", [None, 1000])
+def test_cascade_many_parts_and_pieces(wgs):
+    """11 prefix parts per sequence (the combine folds them 8 at a time) and, at 1,000
+    workgroups, a 2,000-token tail cut into more than 64 pieces (merged 64 records at a
+    time): still the oracle's attention."""
+    from oracle import oracle
+
+    dev = torch.device("cuda:0")
+    tails = [2000, 0, 5, 100, 17, 1, 64, 33, 0, 250, 9, 3]
+    tables, ctx, nblk = _shared_batch(tails=tails, shared_blocks=48, bs=16, seed=11)
+    g = torch.Generator().manual_seed(12)
+    k = torch.randn(nblk * 16, 8, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(nblk * 16, 8, 128, generator=g).to(torch.bfloat16)
+    q = torch.randn(len(tails), 24, 128, generator=g).to(torch.bfloat16)
+    pg = pa.find_prefix_groups(tables, ctx, 16, 24, 8, dev, min_blocks=4, pieces=11)
+    assert pg is not None and pg.pieces == 11
+    args = (q.to(dev), k.to(dev), v.to(dev), tables.to(dev), ctx.to(dev), 16)
+    got = torch.empty(q.shape, dtype=torch.float32, device=dev)
+    pa.paged_decode_attention(*args, out=got, prefix_groups=pg, num_workgroups=wgs)
+    torch.cuda.synchronize()
+    want = oracle.decode_attention(q, k, v, tables, ctx, 16, threads=THREADS)
+    assert (got.cpu() - want).abs().max().item() <= 2e-3
