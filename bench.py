@@ -55,9 +55,10 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-graph", action="store_true", help="time eager calls only")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--only", choices=["cascade", "cow", "append"], default=None,
+    ap.add_argument("--only", choices=["cascade", "cow", "append", "fused"], default=None,
                     help="time one part alone, e.g. under a profiler: cascade decode or "
-                         "the copy-on-write (config c3), the KV append (config c5)")  # fmt: skip
+                         "the copy-on-write (config c3), the KV append or the fused "
+                         "element-wise kernels (config c5)")  # fmt: skip
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 5 plain 1 GiB device-to-device copies: the known-size "
                          "kernel that scales rocprofv3's FETCH_SIZE / WRITE_SIZE")  # fmt: skip
@@ -318,6 +319,61 @@ def bench_append(args, torch) -> dict:
             "append_gbps": round(nbytes / (us * 1e-6) / 1e9, 1)}  # fmt: skip
 
 
+def bench_fused(args, torch) -> dict:
+    """The fused element-wise kernels at config 5's step shape (Llama-3-8B: 2,168 token
+    rows, hidden 4,096, 32 q / 8 KV heads of 128, intermediate 14,336), bf16, graph
+    replay, each beside the PyTorch expression it replaces. Bytes are what the operation
+    must move: RMSNorm x in + out (its per-row rsqrt(mean(x^2)) stays a PyTorch
+    reduction, inside the timed call), RoPE q and k in place + cos and sin (fp32),
+    SiLU x up gate and up in + out."""
+    import torch.nn.functional as F
+
+    from engine.kernels import fused
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    n, hidden, nh, nkv, hd, inter, eps = 2168, 4096, 32, 8, 128, 14336, 1e-5
+    bf = torch.bfloat16
+    x = torch.randn(n, hidden, device=dev, generator=g).to(bf)
+    w = torch.randn(hidden, device=dev, generator=g).to(bf)
+    q = torch.randn(n, nh, hd, device=dev, generator=g).to(bf)
+    k = torch.randn(n, nkv, hd, device=dev, generator=g).to(bf)
+    inv_freq = 1.0 / (500000 ** (torch.arange(0, hd, 2, device=dev).float() / hd))
+    emb = torch.arange(n, device=dev).float()[:, None] * inv_freq
+    emb = torch.cat([emb, emb], -1)
+    cos, sin = emb.cos(), emb.sin()
+    gate = torch.randn(n, inter, device=dev, generator=g).to(bf)
+    up = torch.randn(n, inter, device=dev, generator=g).to(bf)
+
+    def rot(t):
+        h = t.shape[-1] // 2
+        return torch.cat((-t[..., h:], t[..., :h]), -1)
+
+    def torch_rms():
+        xf = x.float()
+        return w * (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)).to(bf)
+
+    def torch_rope():
+        c, s_ = cos[:, None].to(bf), sin[:, None].to(bf)
+        return q * c + rot(q) * s_, k * c + rot(k) * s_
+
+    cases = {
+        "rms_norm": (lambda: fused.rms_norm(x, w, eps), torch_rms, 2 * x.numel() * 2),
+        "rope": (lambda: (fused.rope_(q, cos, sin), fused.rope_(k, cos, sin)), torch_rope,
+                 (q.numel() + k.numel()) * 2 * 2 + 2 * cos.numel() * 4),
+        "silu_mul": (lambda: fused.silu_mul(gate, up), lambda: F.silu(gate) * up,
+                     3 * gate.numel() * 2),
+    }  # fmt: skip
+    res = {}
+    for name, (mine, ref, nbytes) in cases.items():
+        us = graph_us(torch, [mine] * 8, 8 * args.steps, args.warmup)[0]
+        ref_us = graph_us(torch, [ref] * 8, 8 * args.steps, args.warmup)[0]
+        res[name] = {"us": round(us, 2), "bytes": nbytes,
+                     "gbps": round(nbytes / (us * 1e-6) / 1e9, 1),
+                     "torch_us": round(ref_us, 2)}  # fmt: skip
+    return {"config": {"workload": "c5_llama8b_elementwise_bf16", "rows": n}, "fused": res}
+
+
 def bench_mixed(args, torch) -> dict:
     from engine import workloads
     from engine.kernels import paged_attention as pa
@@ -398,7 +454,7 @@ def main() -> int:
 
     import torch
 
-    need = {"cascade": "c3", "cow": "c3", "append": "c5"}.get(args.only)
+    need = {"cascade": "c3", "cow": "c3", "append": "c5", "fused": "c5"}.get(args.only)
     if need and args.config != need:
         print(f"bench.py: --only {args.only} needs --config {need}", file=sys.stderr)
         return 2
@@ -411,6 +467,8 @@ def main() -> int:
         line = {"config": {"workload": step.name}, **bench_cow(torch, step)}
     elif args.only == "append":
         line = bench_append(args, torch)
+    elif args.only == "fused":
+        line = bench_fused(args, torch)
     elif args.config == "c5":
         line = bench_mixed(args, torch)
     else:

@@ -24,9 +24,10 @@ def _rotate_half(x):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
-@pytest.mark.parametrize(("nh", "hd"), [(8, 64), (32, 128), (3, 16)])
+@pytest.mark.parametrize(("nh", "hd"), [(8, 64), (32, 128), (3, 16), (5, 12)])
 def test_rope_is_bitwise_identical(dtype, nh, hd):
-    """HF's q * cos + rotate_half(q) * sin with cos / sin cast to the model dtype."""
+    """HF's q * cos + rotate_half(q) * sin with cos / sin cast to the model dtype (hd 12:
+    half a row is not a whole 16-byte access, so the per-element kernel runs)."""
     _say("rope", dtype, nh, hd)
     g = torch.Generator(device=DEV).manual_seed(0)
     n = 77
@@ -60,17 +61,19 @@ def test_rope_strided_heads_in_place():
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
-def test_silu_mul_is_bitwise_identical(dtype):
-    _say("silu_mul", dtype)
+@pytest.mark.parametrize("shape", [(64, 1000), (7, 999)])
+def test_silu_mul_is_bitwise_identical(dtype, shape):
+    """(7, 999): an element count that is no whole number of 16-byte accesses."""
+    _say("silu_mul", dtype, shape)
     g = torch.Generator(device=DEV).manual_seed(2)
-    gate = (torch.randn(64, 1000, device=DEV, generator=g) * 4).to(dtype)
-    up = torch.randn(64, 1000, device=DEV, generator=g).to(dtype)
+    gate = (torch.randn(*shape, device=DEV, generator=g) * 4).to(dtype)
+    up = torch.randn(*shape, device=DEV, generator=g).to(dtype)
     gate[0, :6] = torch.tensor([0.0, -0.0, 88.0, -88.0, 1e-30, -1e-30]).to(dtype)
     assert torch.equal(fused.silu_mul(gate, up), F.silu(gate) * up)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("dim", [2048, 3072, 100])
+@pytest.mark.parametrize("dim", [2048, 3072, 100, 1000])
 def test_rms_norm_is_bitwise_identical(dtype, dim):
     """Reference tests/test_kernels.py:240-254."""
     _say("rms_norm", dtype, dim)
