@@ -65,15 +65,27 @@ kv_append_kernel(typename Elt<DOUT>::S* __restrict__ k_pool,
 // pool) block: 8 independent 16-byte loads per thread, then the 8 stores.
 // ---------------------------------------------------------------------------------
 
+// Non-temporal store of one copy element (16-byte elements through the native vector type).
+template <typename U> __device__ __forceinline__ void stream_store(U* p, const U& v) {
+  if constexpr (sizeof(U) == 16)
+    __builtin_nontemporal_store(__builtin_bit_cast(u32x4, v), reinterpret_cast<u32x4*>(p));
+  else
+    __builtin_nontemporal_store(v, p);
+}
+
 template <typename U>
 __global__ void __launch_bounds__(256)
 copy_blocks_kernel(char* __restrict__ k_pool, char* __restrict__ v_pool,
                    int64_t layer_stride_bytes, int64_t block_bytes, int64_t num_blocks,
                    const int64_t* __restrict__ mapping) {
   constexpr int kUnroll = 8, kThreads = 256;
-  const int64_t pair = blockIdx.y;
-  const int layer = blockIdx.z >> 1;
-  char* pool = (blockIdx.z & 1) ? v_pool : k_pool;
+  // Grid (chunks, 2 x layers, pairs): consecutive workgroups walk the (layer, K/V)
+  // planes first, so with workgroups dealt round-robin to the 8 XCDs every pair of one
+  // plane lands on the same XCD, whose L2 then serves a source block shared by many
+  // pairs (copy-on-write of one prefix block) to all of them.
+  const int64_t pair = blockIdx.z;
+  const int layer = blockIdx.y >> 1;
+  char* pool = (blockIdx.y & 1) ? v_pool : k_pool;
   const int64_t src = mapping[2 * pair], dst = mapping[2 * pair + 1];
   if (src < 0 || src >= num_blocks || dst < 0 || dst >= num_blocks) return;
   const int64_t n = block_bytes / (int64_t)sizeof(U);
@@ -89,9 +101,9 @@ copy_blocks_kernel(char* __restrict__ k_pool, char* __restrict__ v_pool,
       r[j] = e < n ? s[e] : U{};
     }
 #pragma unroll
-    for (int j = 0; j < kUnroll; ++j) {
+    for (int j = 0; j < kUnroll; ++j) {  // streaming stores: the copies are not read back here
       const int64_t e = base + j * kThreads;
-      if (e < n) d[e] = r[j];
+      if (e < n) stream_store(d + e, r[j]);
     }
   }
 }
@@ -250,7 +262,7 @@ int pkv_copy_blocks(void* k_pool, void* v_pool, int64_t layer_stride_bytes,
     const int64_t n = block_bytes / unit;
     int64_t gx = (n + 256 * 8 - 1) / (256 * 8);
     if (gx > 65535) gx = 65535;
-    return dim3((unsigned)gx, (unsigned)n_pairs, (unsigned)(2 * num_layers));
+    return dim3((unsigned)gx, (unsigned)(2 * num_layers), (unsigned)n_pairs);
   };
   const bool a16 = aligned16(k_pool) && aligned16(v_pool) && layer_stride_bytes % 16 == 0;
   if (a16 && block_bytes % 16 == 0) {
