@@ -756,23 +756,36 @@ __device__ void seq_units(const DecodeArgs& a, int b, int64_t* ub, int64_t* ue, 
   *total = all;
 }
 
-template <int DT, int HD>
+// SP = 1: one wave per (sequence, query head). SP = 2 (batches with few such pairs):
+// two waves per pair, each folding half of the records, their states merged through
+// LDS -- half the dependent round trips for a sequence cut into many pieces.
+template <int DT, int HD, int SP>
 __global__ void __launch_bounds__(256)
 paged_decode_combine_kernel(const DecodeArgs a) {
+  static_assert(SP == 1 || SP == 2, "one or two waves per (sequence, head)");
   constexpr int DPL = HD >= kWave ? HD / kWave : 1;  // head dims per lane
   constexpr int kChunk = PKV_DECODE_COMBINE_CHUNK;    // accumulator rows per load batch
   const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int part = SP == 2 ? (wave & 1) : 0;  // which half of the records (SP = 2)
   // Wave-uniform by construction; readfirstlane lets the compiler keep the plan, record
   // indices and row bases in scalar registers.
-  const int wid = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave);
-  if (wid >= a.batch * a.nh) return;
-  const int b = wid / a.nh, h = wid - b * a.nh;
+  const int wid = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x / kWave / SP) + wave / SP);
+  const bool active = wid < a.batch * a.nh;
+  if (SP == 1 && !active) return;
+  const int pw = active ? wid : 0;  // SP = 2: an idle pair still meets the barrier
+  const int b = pw / a.nh, h = pw - b * a.nh;
 
   const int4 plan = a.desc[b];
   const bool cascade = a.pre_row != nullptr;
-  const int pre = cascade ? a.pre_row[b] : -1;  // fetched with the plan
+  const int pre = cascade && part == 0 ? a.pre_row[b] : -1;  // fetched with the plan
   const int nrec = plan.y;
-  if (nrec <= 1 && !cascade) return;  // written directly by the stream pass
+  // Written directly by the stream pass (or past the batch): nothing to merge.
+  const bool skip = !active || (nrec <= 1 && !cascade);
+  if (SP == 1 && skip) return;
+  // This wave's records [jb, je): all of them, or one half of them.
+  const int jb = part == 0 ? 0 : (nrec + 1) / 2;
+  const int je = SP == 1 || part == 1 ? nrec : (nrec + 1) / 2;
   // The first prefix parts' loads go out before the records are merged.
   PrefixParts<HD, DPL> parts;
   if (pre >= 0) parts.load(a, pre, h, 0);
@@ -794,30 +807,34 @@ paged_decode_combine_kernel(const DecodeArgs a) {
   uint64_t live_bits = 0;
   auto live_block = [&](int j0) {
     const int j = j0 + lane;
-    bool live = j < nrec;
+    bool live = j < je;
     if (!plan.w && live) {
       const int64_t ww = w0 + j;
       live = range_start(ww, total, a.num_wg) < range_start(ww + 1, total, a.num_wg);
     }
     live_bits = __ballot(live);
   };
-  if (nrec <= 1) {
+  if (skip) {
+  } else if (nrec <= 1) {
     // Cascade, finished by the stream pass: its normalised fp32 output and log2
     // normaliser are the state (lse, 1, O); an empty context (-inf) weighs nothing.
+    // (With SP = 2 the first half takes it; the second contributes an empty state.)
+    if (part == 0) {
     const float lt = a.lse[(int64_t)b * a.nh + h];
     mmax = lt;
     lsum = lt == -INFINITY ? 0.f : 1.f;
     const float* t = reinterpret_cast<const float*>(a.out) + b * a.out_sb + (int64_t)h * a.out_sh;
 #pragma unroll
     for (int k = 0; k < DPL; ++k) out_acc[k] = (lane + kWave * k < HD) ? t[lane + kWave * k] : 0.f;
+    }
   } else {
     // Records in blocks of up to 64: lane r of a block loads record j0 + r's (m, l), one
     // wave reduction gives the block's max M, and with every weight 2^(m - M) known up
     // front the accumulator rows stream in chunks of kChunk records, each chunk's loads
     // issued before the previous chunk is consumed (no round trip waits on another).
-    for (int j0 = 0; j0 < nrec; j0 += kWave) {
+    for (int j0 = jb; j0 < je; j0 += kWave) {
       live_block(j0);
-      const int n = min(kWave, nrec - j0);
+      const int n = min(kWave, je - j0);
       auto row_of = [&](int r) -> int64_t {  // r < n: record j0 + r, else record 0
         const bool lv = r < n && ((live_bits >> r) & 1);
         return (lv && j0 + r > 0) ? (w0 + j0 + r) * 2 * a.nh + h : row0;
@@ -861,6 +878,25 @@ paged_decode_combine_kernel(const DecodeArgs a) {
         consume(xb, c + kChunk);
       }
     }
+  }
+  if constexpr (SP == 2) {  // the second half's state joins the first's
+    __shared__ float xch[2][2 + DPL * kWave];
+    float* x = xch[wave >> 1];
+    if (part == 1) {
+      if (lane == 0) x[0] = mmax, x[1] = lsum;
+#pragma unroll
+      for (int k = 0; k < DPL; ++k) x[2 + lane + kWave * k] = out_acc[k];
+    }
+    __syncthreads();
+    if (part == 1 || skip) return;
+    const float mb = x[0];
+    const float mn = fmaxf(mmax, mb);
+    const float mref = mn == -INFINITY ? 0.f : mn;  // both empty: weights 0
+    const float sa = __builtin_amdgcn_exp2f(mmax - mref), sb = __builtin_amdgcn_exp2f(mb - mref);
+    mmax = mn;
+    lsum = lsum * sa + x[1] * sb;
+#pragma unroll
+    for (int k = 0; k < DPL; ++k) out_acc[k] = out_acc[k] * sa + x[2 + lane + kWave * k] * sb;
   }
   if (pre >= 0) {
     parts.fold(mmax, lsum, out_acc);
@@ -960,6 +996,10 @@ template <int DT, int HD, int GPW> const void* decode_kernel() {
     return reinterpret_cast<const void*>(&paged_decode_stream_kernel<DT, HD, GPW>);
 }
 
+// Up to this many (sequence, head) pairs the combine gives each pair two waves (at most
+// 4,096 waves: all resident on a 256-CU part); larger batches get one wave per pair.
+constexpr int kCombineSplitPairs = 2048;
+
 struct LaunchDecode {
   const DecodeArgs* a;
   int wpg, ygrid;
@@ -976,9 +1016,13 @@ struct LaunchDecode {
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || (a->num_wg <= 1 && !a->pre_row)) return e;
-    const int waves = a->batch * a->nh;
-    hipLaunchKernelGGL((paged_decode_combine_kernel<DT, HD>), dim3((unsigned)((waves + 3) / 4)),
-                       dim3(256), 0, st, *a);
+    const int pairs = a->batch * a->nh;  // (sequence, query head) pairs
+    if (pairs <= kCombineSplitPairs)
+      hipLaunchKernelGGL((paged_decode_combine_kernel<DT, HD, 2>), dim3((unsigned)((pairs + 1) / 2)),
+                         dim3(256), 0, st, *a);
+    else
+      hipLaunchKernelGGL((paged_decode_combine_kernel<DT, HD, 1>), dim3((unsigned)((pairs + 3) / 4)),
+                         dim3(256), 0, st, *a);
     return hipGetLastError();
   }
 };
