@@ -474,10 +474,16 @@ template <int DT> __device__ __forceinline__ void unpack16v(u32x4 r, float* f) {
 }
 
 
-template <int DT, int GPW, bool FAST>
+template <int DT, int GPW, bool FAST, int HD>
 __global__ void __launch_bounds__(512)
 paged_decode_mfma_kernel(const DecodeArgs a) {
-  constexpr int HD = 128, TILE = 16;
+  // hd 128: four 32-dim MFMA k-blocks, V rows over all 16 lane columns (8 dims each);
+  // hd 64: two k-blocks, V rows over lane columns 0-7 (the other lanes load nothing).
+  static_assert(HD == 64 || HD == 128, "MFMA decode: hd 64 or 128");
+  constexpr int TILE = 16, KB = HD / 32, VC = HD / 8;
+  // Tiles in flight: at hd 64 a tile is half the bytes, so a third buffer keeps a
+  // wave's bytes in flight up (measured: hd 64 ~3% faster with it, hd 128 ~1% slower).
+  constexpr bool kDeep = HD == 64 || PKV_DECODE_PREFETCH >= 2;
   static_assert(GPW >= 1 && GPW <= 4, "at most 4 query heads per wave");
   using S = typename Elt<DT>::S;
   using MMA = Mfma16x16x32<DT>;
@@ -520,7 +526,7 @@ paged_decode_mfma_kernel(const DecodeArgs a) {
     {
       const S* qp = reinterpret_cast<const S*>(a.q) + b * a.q_sb + (int64_t)(h0 + col) * a.q_sh + 8 * grp;
 #pragma unroll
-      for (int m = 0; m < 4; ++m)
+      for (int m = 0; m < KB; ++m)
         qb[m] = col < GPW ? *reinterpret_cast<const u32x4*>(qp + 32 * m) : u32x4{0, 0, 0, 0};
     }
 
@@ -553,9 +559,9 @@ paged_decode_mfma_kernel(const DecodeArgs a) {
         const S* vt = vbase + slot0 * a.kv_ss;
         if (live == TILE) {  // full tile: every lane loads, no predication
 #pragma unroll
-          for (int m = 0; m < 4; ++m) kr[m] = load_kv16v(kt + k_off + 32 * m);
+          for (int m = 0; m < KB; ++m) kr[m] = load_kv16v(kt + k_off + 32 * m);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) vr[r] = load_kv16v(vt + v_off[r]);
+          for (int r = 0; r < 4; ++r) vr[r] = col < VC ? load_kv16v(vt + v_off[r]) : z;
           return 0xFu;
         }
         if (live == 0) {  // block id outside the pool: the tile is masked
@@ -567,12 +573,12 @@ paged_decode_mfma_kernel(const DecodeArgs a) {
         // token (finite data) and are masked out of the softmax (P = 0).
         const int kt_tok = min(col, live - 1);
 #pragma unroll
-        for (int m = 0; m < 4; ++m)
+        for (int m = 0; m < KB; ++m)
           kr[m] = load_kv16v(kt + kt_tok * a.kv_ss + 8 * grp + 32 * m);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int tok = 4 * grp + r;
-          vr[r] = load_kv16v(vt + min(tok, live - 1) * a.kv_ss + 8 * col);
+          vr[r] = col < VC ? load_kv16v(vt + min(tok, live - 1) * a.kv_ss + 8 * col) : z;
           ok |= (unsigned)(tok < live) << r;
         }
       } else {
@@ -584,7 +590,7 @@ paged_decode_mfma_kernel(const DecodeArgs a) {
         const bool kon = p < t1 && sl >= 0 && sl < a.num_slots;
         const int64_t kslot = kon ? sl : -1;
 #pragma unroll
-        for (int m = 0; m < 4; ++m)
+        for (int m = 0; m < KB; ++m)
           kr[m] = kon ? load_kv16v(kbase + kslot * a.kv_ss + 8 * grp + 32 * m) : z;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -593,7 +599,7 @@ paged_decode_mfma_kernel(const DecodeArgs a) {
           const int hi = __shfl((int)(kslot >> 32), src);
           const int64_t vs = ((int64_t)hi << 32) | (uint32_t)lo;
           const bool on = vs >= 0;
-          vr[r] = on ? load_kv16v(vbase + vs * a.kv_ss + 8 * col) : z;
+          vr[r] = on && col < VC ? load_kv16v(vbase + vs * a.kv_ss + 8 * col) : z;
           ok |= (unsigned)on << r;
         }
       }
@@ -611,7 +617,7 @@ paged_decode_mfma_kernel(const DecodeArgs a) {
     auto tile = [&](const u32x4* kr, const u32x4* vr, unsigned ok) {
       f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int m = 0; m < 4; ++m) s = MMA::mma(kr[m], qb[m], s);
+      for (int m = 0; m < KB; ++m) s = MMA::mma(kr[m], qb[m], s);
       float p[4];
       float mx = -INFINITY;
 #pragma unroll
@@ -646,34 +652,34 @@ paged_decode_mfma_kernel(const DecodeArgs a) {
 
     if (t0 < t1) {
       load_table(block_of(t0));
-#if PKV_DECODE_PREFETCH >= 2
-      // Three tile buffers in rotation: two tiles in flight while one is reduced.
-      u32x4 k0[4], v0[4], k1[4], v1[4], k2[4], v2[4];
-      unsigned ok0 = load_tile(t0, k0, v0);
-      unsigned ok1 = load_tile(t0 + TILE, k1, v1);
-      unsigned ok2;
-      for (int tb = t0; tb < t1; tb += 3 * TILE) {
-        ok2 = load_tile(tb + 2 * TILE, k2, v2);
-        tile(k0, v0, ok0);
-        if (tb + TILE >= t1) break;
-        ok0 = load_tile(tb + 3 * TILE, k0, v0);
-        tile(k1, v1, ok1);
-        if (tb + 2 * TILE >= t1) break;
-        ok1 = load_tile(tb + 4 * TILE, k1, v1);
-        tile(k2, v2, ok2);
+      if constexpr (kDeep) {
+        // Three tile buffers in rotation: two tiles in flight while one is reduced.
+        u32x4 k0[4], v0[4], k1[4], v1[4], k2[4], v2[4];
+        unsigned ok0 = load_tile(t0, k0, v0);
+        unsigned ok1 = load_tile(t0 + TILE, k1, v1);
+        unsigned ok2;
+        for (int tb = t0; tb < t1; tb += 3 * TILE) {
+          ok2 = load_tile(tb + 2 * TILE, k2, v2);
+          tile(k0, v0, ok0);
+          if (tb + TILE >= t1) break;
+          ok0 = load_tile(tb + 3 * TILE, k0, v0);
+          tile(k1, v1, ok1);
+          if (tb + 2 * TILE >= t1) break;
+          ok1 = load_tile(tb + 4 * TILE, k1, v1);
+          tile(k2, v2, ok2);
+        }
+      } else {
+        // Two tile buffers in ping-pong: the next tile is in flight while one is reduced.
+        u32x4 ka[4], va[4], kb2[4], vb2[4];
+        unsigned oka = load_tile(t0, ka, va);
+        for (int tb = t0; tb < t1; tb += 2 * TILE) {
+          const unsigned okb = load_tile(tb + TILE, kb2, vb2);
+          tile(ka, va, oka);
+          if (tb + TILE >= t1) break;
+          oka = load_tile(tb + 2 * TILE, ka, va);
+          tile(kb2, vb2, okb);
+        }
       }
-#else
-      // Two tile buffers in ping-pong: the next tile is in flight while one is reduced.
-      u32x4 ka[4], va[4], kb2[4], vb2[4];
-      unsigned oka = load_tile(t0, ka, va);
-      for (int tb = t0; tb < t1; tb += 2 * TILE) {
-        const unsigned okb = load_tile(tb + TILE, kb2, vb2);
-        tile(ka, va, oka);
-        if (tb + TILE >= t1) break;
-        oka = load_tile(tb + 2 * TILE, ka, va);
-        tile(kb2, vb2, okb);
-      }
-#endif
     }
 
     // Totals: l over the four rows of each column, acc over the four rows.
@@ -689,7 +695,7 @@ paged_decode_mfma_kernel(const DecodeArgs a) {
       mh[g] = row_bcast(m_run, g);
     }
 
-    if (grp == 0) {  // lane c writes head dims 8c .. 8c + 7
+    if (grp == 0 && col < VC) {  // lane c writes head dims 8c .. 8c + 7
       const int d0 = 8 * col;
       if (whole) {
 #pragma unroll
@@ -987,11 +993,11 @@ template <class F> hipError_t by_dtype(int dt, int hd, int gpw, const F& f) {
 // The MFMA kernel serves 16-bit K/V at head_dim 128; every other shape uses the
 // generic stream kernel.
 template <int DT, int HD> constexpr bool use_mfma() {
-  return DT != PKV_F32 && HD == 128 && PKV_DECODE_USE_MFMA;
+  return DT != PKV_F32 && (HD == 128 || HD == 64) && PKV_DECODE_USE_MFMA;
 }
 template <int DT, int HD, int GPW> const void* decode_kernel() {
   if constexpr (use_mfma<DT, HD>())
-    return reinterpret_cast<const void*>(&paged_decode_mfma_kernel<DT, GPW, true>);
+    return reinterpret_cast<const void*>(&paged_decode_mfma_kernel<DT, GPW, true, HD>);
   else
     return reinterpret_cast<const void*>(&paged_decode_stream_kernel<DT, HD, GPW>);
 }
@@ -1008,9 +1014,9 @@ struct LaunchDecode {
     const dim3 grid((unsigned)a->num_wg, (unsigned)ygrid), block(kWave * wpg);
     if constexpr (use_mfma<DT, HD>()) {
       if (a->bs % 16 == 0)
-        hipLaunchKernelGGL((paged_decode_mfma_kernel<DT, GPW, true>), grid, block, 0, st, *a);
+        hipLaunchKernelGGL((paged_decode_mfma_kernel<DT, GPW, true, HD>), grid, block, 0, st, *a);
       else
-        hipLaunchKernelGGL((paged_decode_mfma_kernel<DT, GPW, false>), grid, block, 0, st, *a);
+        hipLaunchKernelGGL((paged_decode_mfma_kernel<DT, GPW, false, HD>), grid, block, 0, st, *a);
     } else {
       hipLaunchKernelGGL((paged_decode_stream_kernel<DT, HD, GPW>), grid, block, 0, st, *a);
     }
@@ -1034,6 +1040,8 @@ struct QueryDecode {
   int* tile;
   int* per_cu;  // may be null: tile only
   template <int DT, int HD, int GPW> hipError_t run() const {
+    static_assert(!use_mfma<DT, HD>() || DecodeShape<DT, HD>::TILE == 16,
+                  "the MFMA kernel's unit is 16 tokens");
     *tile = DecodeShape<DT, HD>::TILE;
     if (!per_cu) return hipSuccess;
     return hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, decode_kernel<DT, HD, GPW>(),
