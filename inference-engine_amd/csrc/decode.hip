@@ -477,13 +477,13 @@ template <int DT> __device__ __forceinline__ void unpack16v(u32x4 r, float* f) {
 template <int DT, int GPW, bool FAST, int HD>
 __global__ void __launch_bounds__(512)
 paged_decode_mfma_kernel(const DecodeArgs a) {
-  // hd 128: four 32-dim MFMA k-blocks, V rows over all 16 lane columns (8 dims each);
-  // hd 64: two k-blocks, V rows over lane columns 0-7 (the other lanes load nothing).
+  // hd 128: a step is one 16-token tile, four 32-dim MFMA k-blocks, V rows over all 16
+  // lane columns (8 dims each). hd 64: a step is two 16-token sub-tiles (the same 8 KB
+  // per wave in flight as at hd 128), two k-blocks each, the V rows of sub-tile u on
+  // lane columns 8u .. 8u + 7, the two halves of the accumulator added at the end.
   static_assert(HD == 64 || HD == 128, "MFMA decode: hd 64 or 128");
-  constexpr int TILE = 16, KB = HD / 32, VC = HD / 8;
-  // Tiles in flight: at hd 64 a tile is half the bytes, so a third buffer keeps a
-  // wave's bytes in flight up (measured: hd 64 ~3% faster with it, hd 128 ~1% slower).
-  constexpr bool kDeep = HD == 64 || PKV_DECODE_PREFETCH >= 2;
+  constexpr int TILE = 16, KB = HD / 32, VC = HD / 8, NS = 128 / HD, STEP = NS * TILE;
+  constexpr bool kDeep = PKV_DECODE_PREFETCH >= 2;
   static_assert(GPW >= 1 && GPW <= 4, "at most 4 query heads per wave");
   using S = typename Elt<DT>::S;
   using MMA = Mfma16x16x32<DT>;
@@ -507,7 +507,7 @@ paged_decode_mfma_kernel(const DecodeArgs a) {
   const int64_t k_off = col * a.kv_ss + 8 * grp;
   int64_t v_off[4];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) v_off[r] = (4 * grp + r) * a.kv_ss + 8 * col;
+  for (int r = 0; r < 4; ++r) v_off[r] = (4 * grp + r) * a.kv_ss + 8 * (HD == 64 ? (col & 7) : col);
 
   for (int64_t u = rs; u < re && b < a.batch; ++b) {
     const int n = clamped_ctx(a, b);
@@ -606,6 +606,82 @@ paged_decode_mfma_kernel(const DecodeArgs a) {
       return ok;
     };
 
+    // hd 64: sub-tile u's K into kr[KB u ..] and V rows on lane columns 8u .. 8u + 7
+    // (other lanes keep theirs); returns bit r set when token 4*grp + r is live.
+    const bool vlane0 = col < 8;  // hd 64: this lane's V rows come from sub-tile 0
+    auto load_sub = [&](int tb, u32x4* kr, u32x4* vr, int u) -> unsigned {
+      const u32x4 z = {0, 0, 0, 0};
+      const bool vmine = (col >> 3) == u;
+      const int vd = 8 * (col & 7);
+      kr += KB * u;
+      if (tb >= t1) {
+#pragma unroll
+        for (int i = 0; i < KB; ++i) kr[i] = z;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) vr[r] = vmine ? z : vr[r];
+        return 0;
+      }
+      if (block_of(min(tb + TILE, t1) - 1) - cb >= kWave) load_table(block_of(tb));
+      unsigned ok = 0;
+      if constexpr (FAST) {
+        const int blk = block_of(tb);
+        const int bid = __builtin_amdgcn_readlane(tbl, blk - cb);
+        const int64_t slot0 = (int64_t)bid * a.bs + (tb - blk * a.bs);
+        const int live = (bid >= 0 && slot0 + TILE <= a.num_slots) ? min(TILE, t1 - tb) : 0;
+        const S* kt = kbase + slot0 * a.kv_ss;
+        const S* vt = vbase + slot0 * a.kv_ss;
+        if (live == TILE) {  // full sub-tile: precomputed offsets, no clamping
+#pragma unroll
+          for (int m = 0; m < KB; ++m) kr[m] = load_kv16v(kt + k_off + 32 * m);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) vr[r] = vmine ? load_kv16v(vt + v_off[r]) : vr[r];
+          return 0xFu;
+        }
+        if (live == 0) {
+#pragma unroll
+          for (int i = 0; i < KB; ++i) kr[i] = z;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) vr[r] = vmine ? z : vr[r];
+          return 0;
+        }
+        const int kt_tok = min(col, live - 1);
+#pragma unroll
+        for (int m = 0; m < KB; ++m) kr[m] = load_kv16v(kt + kt_tok * a.kv_ss + 8 * grp + 32 * m);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int tok = 4 * grp + r;
+          vr[r] = vmine ? load_kv16v(vt + min(tok, live - 1) * a.kv_ss + vd) : vr[r];
+          ok |= (unsigned)(tok < live) << r;
+        }
+      } else {
+        const int p = tb + col;
+        const int blk = block_of(p);
+        const int bid = __shfl(tbl, blk - cb);
+        const int64_t sl = (int64_t)bid * a.bs + (p - blk * a.bs);
+        const bool kon = p < t1 && sl >= 0 && sl < a.num_slots;
+        const int64_t kslot = kon ? sl : -1;
+#pragma unroll
+        for (int m = 0; m < KB; ++m)
+          kr[m] = kon ? load_kv16v(kbase + kslot * a.kv_ss + 8 * grp + 32 * m) : z;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int src = 4 * grp + r;
+          const int lo = __shfl((int)(kslot & 0xFFFFFFFF), src);
+          const int hi = __shfl((int)(kslot >> 32), src);
+          const int64_t vs = ((int64_t)hi << 32) | (uint32_t)lo;
+          const bool on = vs >= 0;
+          vr[r] = vmine ? (on ? load_kv16v(vbase + vs * a.kv_ss + vd) : z) : vr[r];
+          ok |= (unsigned)on << r;
+        }
+      }
+      return ok;
+    };
+    // A step's loads; ok bits 4u .. 4u + 3 mark sub-tile u's live tokens.
+    auto load_step = [&](int tb, u32x4* kr, u32x4* vr) -> unsigned {
+      if constexpr (NS == 1) return load_tile(tb, kr, vr);
+      else return load_sub(tb, kr, vr, 0) | (load_sub(tb + TILE, kr, vr, 1) << 4);
+    };
+
     float m_run = -INFINITY;  // running max of head column col (same in all 4 rows)
     float l_run = 0.f;        // this row's share of the running sum
     float acc[GPW][8];
@@ -615,37 +691,83 @@ paged_decode_mfma_kernel(const DecodeArgs a) {
       for (int d = 0; d < 8; ++d) acc[g][d] = 0.f;
 
     auto tile = [&](const u32x4* kr, const u32x4* vr, unsigned ok) {
-      f32x4 s = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int m = 0; m < KB; ++m) s = MMA::mma(kr[m], qb[m], s);
-      float p[4];
-      float mx = -INFINITY;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        p[r] = ((ok >> r) & 1u) ? s[r] * a.scale_log2 : -INFINITY;
-        mx = fmaxf(mx, p[r]);
-      }
-      mx = rows_max(mx);
-      const float mn = fmaxf(m_run, mx);
-      const float mref = mn == -INFINITY ? 0.f : mn;  // all masked so far: stay at 0
-      const float alpha = __builtin_amdgcn_exp2f(m_run - mref);
-      m_run = mn;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) p[r] = __builtin_amdgcn_exp2f(p[r] - mref);
-      l_run = __builtin_fmaf(l_run, alpha, (p[0] + p[1]) + (p[2] + p[3]));
-      float vf[4][8];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) unpack16v<DT>(vr[r], vf[r]);
-#pragma unroll
-      for (int g = 0; g < GPW; ++g) {
-        const float al = row_bcast(alpha, g);
-#pragma unroll
-        for (int d = 0; d < 8; ++d) acc[g][d] *= al;
-#pragma unroll
+      if constexpr (NS == 1) {
+        f32x4 s = {0.f, 0.f, 0.f, 0.f};
+  #pragma unroll
+        for (int m = 0; m < KB; ++m) s = MMA::mma(kr[m], qb[m], s);
+        float p[4];
+        float mx = -INFINITY;
+  #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float pr = row_bcast(p[r], g);
+          p[r] = ((ok >> r) & 1u) ? s[r] * a.scale_log2 : -INFINITY;
+          mx = fmaxf(mx, p[r]);
+        }
+        mx = rows_max(mx);
+        const float mn = fmaxf(m_run, mx);
+        const float mref = mn == -INFINITY ? 0.f : mn;  // all masked so far: stay at 0
+        const float alpha = __builtin_amdgcn_exp2f(m_run - mref);
+        m_run = mn;
+  #pragma unroll
+        for (int r = 0; r < 4; ++r) p[r] = __builtin_amdgcn_exp2f(p[r] - mref);
+        l_run = __builtin_fmaf(l_run, alpha, (p[0] + p[1]) + (p[2] + p[3]));
+        float vf[4][8];
+  #pragma unroll
+        for (int r = 0; r < 4; ++r) unpack16v<DT>(vr[r], vf[r]);
+  #pragma unroll
+        for (int g = 0; g < GPW; ++g) {
+          const float al = row_bcast(alpha, g);
+  #pragma unroll
+          for (int d = 0; d < 8; ++d) acc[g][d] *= al;
+  #pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float pr = row_bcast(p[r], g);
+  #pragma unroll
+            for (int d = 0; d < 8; ++d) acc[g][d] = __builtin_fmaf(pr, vf[r][d], acc[g][d]);
+          }
+        }
+      } else {
+        float p[2][4];
+        float mx = -INFINITY;
 #pragma unroll
-          for (int d = 0; d < 8; ++d) acc[g][d] = __builtin_fmaf(pr, vf[r][d], acc[g][d]);
+        for (int u = 0; u < 2; ++u) {
+          f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int m = 0; m < KB; ++m) s = MMA::mma(kr[KB * u + m], qb[m], s);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            p[u][r] = ((ok >> (4 * u + r)) & 1u) ? s[r] * a.scale_log2 : -INFINITY;
+            mx = fmaxf(mx, p[u][r]);
+          }
+        }
+        mx = rows_max(mx);
+        const float mn = fmaxf(m_run, mx);
+        const float mref = mn == -INFINITY ? 0.f : mn;  // all masked so far: stay at 0
+        const float alpha = __builtin_amdgcn_exp2f(m_run - mref);
+        m_run = mn;
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) p[u][r] = __builtin_amdgcn_exp2f(p[u][r] - mref);
+        l_run = __builtin_fmaf(l_run, alpha, ((p[0][0] + p[0][1]) + (p[0][2] + p[0][3])) +
+                                             ((p[1][0] + p[1][1]) + (p[1][2] + p[1][3])));
+        float vf[4][8];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) unpack16v<DT>(vr[r], vf[r]);
+#pragma unroll
+        for (int g = 0; g < GPW; ++g) {
+          const float al = row_bcast(alpha, g);
+#pragma unroll
+          for (int d = 0; d < 8; ++d) acc[g][d] *= al;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            // This lane's V rows are sub-tile (col / 8)'s: that sub-tile's weights. Both
+            // broadcasts run in every lane before the select: a DPP broadcast on the
+            // untaken side would read its source lane (column g < 8) while inactive.
+            const float p0 = row_bcast(p[0][r], g), p1 = row_bcast(p[1][r], g);
+            const float pr = vlane0 ? p0 : p1;
+#pragma unroll
+            for (int d = 0; d < 8; ++d) acc[g][d] = __builtin_fmaf(pr, vf[r][d], acc[g][d]);
+          }
         }
       }
     };
@@ -655,39 +777,43 @@ paged_decode_mfma_kernel(const DecodeArgs a) {
       if constexpr (kDeep) {
         // Three tile buffers in rotation: two tiles in flight while one is reduced.
         u32x4 k0[4], v0[4], k1[4], v1[4], k2[4], v2[4];
-        unsigned ok0 = load_tile(t0, k0, v0);
-        unsigned ok1 = load_tile(t0 + TILE, k1, v1);
+        unsigned ok0 = load_step(t0, k0, v0);
+        unsigned ok1 = load_step(t0 + STEP, k1, v1);
         unsigned ok2;
-        for (int tb = t0; tb < t1; tb += 3 * TILE) {
-          ok2 = load_tile(tb + 2 * TILE, k2, v2);
+        for (int tb = t0; tb < t1; tb += 3 * STEP) {
+          ok2 = load_step(tb + 2 * STEP, k2, v2);
           tile(k0, v0, ok0);
-          if (tb + TILE >= t1) break;
-          ok0 = load_tile(tb + 3 * TILE, k0, v0);
+          if (tb + STEP >= t1) break;
+          ok0 = load_step(tb + 3 * STEP, k0, v0);
           tile(k1, v1, ok1);
-          if (tb + 2 * TILE >= t1) break;
-          ok1 = load_tile(tb + 4 * TILE, k1, v1);
+          if (tb + 2 * STEP >= t1) break;
+          ok1 = load_step(tb + 4 * STEP, k1, v1);
           tile(k2, v2, ok2);
         }
       } else {
         // Two tile buffers in ping-pong: the next tile is in flight while one is reduced.
         u32x4 ka[4], va[4], kb2[4], vb2[4];
-        unsigned oka = load_tile(t0, ka, va);
-        for (int tb = t0; tb < t1; tb += 2 * TILE) {
-          const unsigned okb = load_tile(tb + TILE, kb2, vb2);
+        unsigned oka = load_step(t0, ka, va);
+        for (int tb = t0; tb < t1; tb += 2 * STEP) {
+          const unsigned okb = load_step(tb + STEP, kb2, vb2);
           tile(ka, va, oka);
-          if (tb + TILE >= t1) break;
-          oka = load_tile(tb + 2 * TILE, ka, va);
+          if (tb + STEP >= t1) break;
+          oka = load_step(tb + 2 * STEP, ka, va);
           tile(kb2, vb2, okb);
         }
       }
     }
 
-    // Totals: l over the four rows of each column, acc over the four rows.
+    // Totals: l over the four rows of each column, acc over the four rows (and, at hd 64,
+    // over the two sub-tiles' lane columns c and c + 8, which hold the same dims).
     const float l_tot = rows_sum(l_run);
 #pragma unroll
     for (int g = 0; g < GPW; ++g)
 #pragma unroll
-      for (int d = 0; d < 8; ++d) acc[g][d] = rows_sum(acc[g][d]);
+      for (int d = 0; d < 8; ++d) {
+        acc[g][d] = rows_sum(acc[g][d]);
+        if constexpr (NS == 2) acc[g][d] += __shfl_xor(acc[g][d], 8);
+      }
     float lh[GPW], mh[GPW];
 #pragma unroll
     for (int g = 0; g < GPW; ++g) {
