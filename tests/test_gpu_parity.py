@@ -411,3 +411,17 @@ def test_native_library_is_loaded_from_tree():
     lib = _native.lib()
     assert os.path.samefile(lib._name, _native.LIB_PATH)
     assert pa.available(DEV)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("block_size", [4, 16, 32])
+@pytest.mark.parametrize("wgs", [None, 1, 7])
+def test_decode_hd64_two_subtile_steps(dtype, block_size, wgs):
+    """hd 64 steps through two 16-token sub-tiles at a time (V rows of the second on the
+    other half of the lane columns): the Llama-3.2-1B shape (32 q / 8 KV heads), long and
+    ragged contexts so both sub-tiles carry live tokens, whole sequences (one workgroup)
+    and cut ones."""
+    _say("decode hd64 sub-tiles", dtype, block_size, wgs)
+    step = workloads.custom([1, 15, 16, 17, 31, 32, 33, 300, 777, 1500], 32, 8, 64,
+                            block_size, dtype, DEV, seed=64 + block_size)  # fmt: skip
+    _check_attention(step, wgs=wgs, what=f"hd64 bs{block_size} wgs{wgs}")
