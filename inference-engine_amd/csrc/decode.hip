@@ -424,11 +424,13 @@ paged_decode_stream_kernel(const DecodeArgs a) {
 }
 
 // ---------------------------------------------------------------------------------
-// MFMA variant of the stream pass for 16-bit K/V at head_dim 128 (the Llama-3 shapes).
+// MFMA variant of the stream pass for 16-bit K/V at head_dim 128 (the Llama-3 shapes)
+// and 64 (Llama-3.2-1B).
 //
 // Same stream-K ranges, records and outputs as paged_decode_stream_kernel; only the
 // per-tile arithmetic differs. A tile is 16 tokens. Lane l is (col = l % 16, grp =
-// l / 16).
+// l / 16). (hd 64 takes two tiles per step: two k-blocks per score block, and the V
+// rows of the second tile on lane columns 8 .. 15; see the kernel.)
 //   * Scores on the matrix cores: S[16 tokens x 16 cols] = K_tile . Q^T with four
 //     v_mfma_f32_16x16x32 (32 head dims each). A operand: lane (t, g) holds K[token t]
 //     dims 32m + 8g .. +8 (one 16-byte load per MFMA); B operand: lane (j, g) holds
