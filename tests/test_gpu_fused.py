@@ -100,3 +100,32 @@ def test_rms_norm_mixed_dtypes_and_shapes():
     xsf = xs.float()
     want = ws * (xsf * torch.rsqrt(xsf.pow(2).mean(-1, keepdim=True) + 1e-5)).to(xs.dtype)
     assert torch.equal(fused.rms_norm(xs, ws, 1e-5), want)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_fused_misaligned_views_take_the_per_element_path(dtype):
+    """Views one element off a 16-byte boundary cannot use the 16-byte kernels; the
+    per-element ones run and stay bitwise identical to PyTorch."""
+    _say("fused misaligned", dtype)
+    g = torch.Generator(device=DEV).manual_seed(5)
+    # SiLU x up on flat views starting one element in
+    base_g = (torch.randn(8 * 512 + 1, device=DEV, generator=g) * 4).to(dtype)
+    base_u = torch.randn(8 * 512 + 1, device=DEV, generator=g).to(dtype)
+    gate, up = base_g[1:], base_u[1:]
+    assert torch.equal(fused.silu_mul(gate, up), F.silu(gate) * up)
+    # RMSNorm over rows whose first element is misaligned
+    xb = (torch.randn(40 * 256 + 1, device=DEV, generator=g) * 3).to(dtype)
+    x = xb[1:].view(40, 256)
+    w = torch.randn(257, device=DEV, generator=g).to(dtype)[1:]
+    xf = x.float()
+    want = w * (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-5)).to(dtype)
+    assert torch.equal(fused.rms_norm(x, w, 1e-5), want)
+    # RoPE on a head view starting one element in
+    n, nh, hd = 9, 4, 64
+    qb = torch.randn(n * nh * hd + 1, device=DEV, generator=g).to(dtype)
+    q = qb[1:].view(n, nh, hd)
+    emb = torch.randn(n, hd, device=DEV, generator=g)
+    cos, sin = emb.cos(), emb.sin()
+    want_q = q * cos[:, None].to(dtype) + _rotate_half(q) * sin[:, None].to(dtype)
+    fused.rope_(q, cos, sin)
+    assert torch.equal(q, want_q)
