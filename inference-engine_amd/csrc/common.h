@@ -40,6 +40,9 @@ constexpr int kWave = 64;
 #ifndef PKV_DECODE_COMBINE_CHUNK
 #define PKV_DECODE_COMBINE_CHUNK 4
 #endif
+#ifndef PKV_DECODE_COMBINE_SPLIT_PAIRS
+#define PKV_DECODE_COMBINE_SPLIT_PAIRS 2048
+#endif
 #ifndef PKV_PREFILL_SETPRIO
 #define PKV_PREFILL_SETPRIO 0
 #endif

@@ -1132,7 +1132,7 @@ template <int DT, int HD, int GPW> const void* decode_kernel() {
 
 // Up to this many (sequence, head) pairs the combine gives each pair two waves (at most
 // 4,096 waves: all resident on a 256-CU part); larger batches get one wave per pair.
-constexpr int kCombineSplitPairs = 2048;
+constexpr int kCombineSplitPairs = PKV_DECODE_COMBINE_SPLIT_PAIRS;
 
 struct LaunchDecode {
   const DecodeArgs* a;
