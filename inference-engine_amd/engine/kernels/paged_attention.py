@@ -264,6 +264,8 @@ def paged_decode_attention(
     lib = _native.lib()
     cascade = prefix_groups is not None and q.dtype in (torch.bfloat16, torch.float16) \
         and hd in PREFILL_HEAD_DIMS  # fmt: skip
+    if cascade:
+        _check_prefix_groups(prefix_groups, b, dev, what)
     query = lib.pkv_cascade_workspace_bytes if cascade else lib.pkv_decode_workspace_bytes
     ws_bytes = query(num_workgroups, b, nh, hd)
     ws = None
@@ -292,6 +294,26 @@ def paged_decode_attention(
     )  # fmt: skip
     _native.check(status, what)
     return out
+
+
+def _check_prefix_groups(pg: PrefixGroups, batch: int, dev: torch.device, what: str) -> None:
+    """The kernels read first_block[b] and prefix_row[b] for every sequence b and the
+    prefix pass's tables by chunk: a PrefixGroups built for another step (another batch
+    size or order) must be rejected before launch, not read out of bounds."""
+    fields = {"first_block": pg.first_block, "prefix_row": pg.prefix_row, "q_rows": pg.q_rows,
+              "cu_q": pg.cu_q, "ctx": pg.ctx, "tables": pg.tables}  # fmt: skip
+    for name, t in fields.items():
+        if t.dtype != torch.int32 or t.device != dev or not t.is_contiguous():
+            raise ValueError(f"{what}: prefix_groups.{name} must be a contiguous int32 "
+                             f"tensor on {dev}")  # fmt: skip
+    if pg.first_block.shape != (batch,) or pg.prefix_row.shape != (batch,):
+        raise ValueError(f"{what}: prefix_groups built for {pg.first_block.numel()} "
+                         f"sequences, called with {batch}")  # fmt: skip
+    chunks = pg.ctx.numel()
+    if pg.pieces < 1 or pg.members < 1 or chunks % pg.pieces or \
+            pg.cu_q.shape != (chunks + 1,) or pg.tables.dim() != 2 or \
+            pg.tables.shape[0] != chunks or pg.q_rows.shape != (pg.pieces * pg.members,):  # fmt: skip
+        raise ValueError(f"{what}: prefix_groups fields disagree with each other")
 
 
 def _cascade_prefix(q, k_cache, v_cache, block_size,
@@ -359,7 +381,7 @@ def paged_prefill_attention(
     *,
     out: torch.Tensor | None = None,
 ) -> torch.Tensor:
-    """Bottom-right causal attention of prompt chunks over the paged pool (MFMA).
+    """Bottom-right causal attention of prompt chunks over the paged pool.
 
     q: [T, nh, hd] -- the query tokens of all chunks back to back; chunk c owns rows
     cu_seqlens_q[c] .. cu_seqlens_q[c+1]-1. block_tables: int32 [C, W];
@@ -371,6 +393,10 @@ def paged_prefill_attention(
     of the reference (engine/model/layers.py:246-253; metadata built at
     engine/runtime/paged_cache.py:182-202) without materialising the gathered K/V.
     ``max_query_len`` bounds every chunk (it sizes the grid: one graph per bucket).
+    16-bit caches at head_dim 32-256 run on the matrix cores (the reference's
+    FlashAttention shapes); fp32 caches and head_dim 16 (the reference's per-chunk SDPA
+    path, layers.py:254-265) on a VALU kernel that stages each K/V tile in LDS once per
+    16 query tokens.
     """
     what = "paged_prefill_attention"
     dev = _native.require_gpu(what, q, k_cache, v_cache, block_tables, context_lens,
@@ -381,11 +407,11 @@ def paged_prefill_attention(
     nkv = k_cache.shape[1]
     if k_cache.shape[2] != hd or nh % nkv:
         raise ValueError(f"{what}: cache {tuple(k_cache.shape)} does not fit q {tuple(q.shape)}")
-    if hd not in PREFILL_HEAD_DIMS:
-        raise ValueError(f"{what}: head_dim {hd} not in {PREFILL_HEAD_DIMS}")
-    if q.dtype not in (torch.bfloat16, torch.float16) or k_cache.dtype != q.dtype or \
-            v_cache.dtype != q.dtype:  # fmt: skip
-        raise TypeError(f"{what}: q and caches must share one dtype, bfloat16 or float16")
+    if hd not in SUPPORTED_HEAD_DIMS:
+        raise ValueError(f"{what}: head_dim {hd} not in {SUPPORTED_HEAD_DIMS}")
+    if k_cache.dtype != q.dtype or v_cache.dtype != q.dtype:
+        raise TypeError(f"{what}: q {q.dtype} and caches {k_cache.dtype}/{v_cache.dtype} "
+                        "must share one dtype")  # fmt: skip
     if k_cache.stride() != v_cache.stride() or k_cache.stride(2) != 1:
         raise ValueError(f"{what}: k_cache and v_cache need equal strides, unit in head_dim")
     for name, x in (("block_tables", block_tables), ("context_lens", context_lens),

@@ -1,80 +1,110 @@
-"""Decode steps as hipGraph replays (reference engine/runtime/cuda_graphs.py:20-108,
-``DecodeGraphs``): the whole forward pass of a decode step is captured once per
-batch-size bucket and replayed, so hundreds of launches become one.
+"""Decode and mixed steps as hipGraph replays, with the constructor and ``run`` signatures
+of the reference's ``DecodeGraphs`` / ``MixedGraphs`` (engine/runtime/cuda_graphs.py:23-108,
+:116-228). torch's CUDA graph API is hipGraph on ROCm.
 
-Graphs need fixed shapes and addresses, so every input lives in a static buffer sized
-for the largest bucket; a step of B sequences copies its token ids, positions, block
-tables and context lengths in, pads to the next bucket and replays. Padding rows have
-context length 1 and a table of the scratch block (a block the allocator never hands
-out), so they write and read only that block.
-
-Differences from the reference: the slot mapping is not copied in -- the captured step
-starts with the HIP slot builder (``decode_slots``), which derives every sequence's
-new slot from the tables and lengths already on the device -- and the attention inside
-is this build's HIP decode kernel, whose grid depends only on static shapes (context
-lengths are read from device memory), so one graph serves every length.
+Both capture the whole step once per size bucket and replay it: every kernel of this
+build reads the step's metadata from device memory and sizes its grid from static
+bounds only, so one graph serves every context length and every mix of sequences that
+fits the bucket. Padding rows write and read only the scratch block, a block the
+allocator never hands out.
 """
 
 from __future__ import annotations
 
+import bisect
 from collections.abc import Callable, Sequence
 
+import numpy as np
 import torch
 
 from engine.runtime.paged_cache import PagedBatch, PagedKVCache, decode_slots
 
+# Batch-size buckets of decode graphs (the reference's table).
 BUCKETS = (1, 2, 4, 8, 16, 24, 32, 48, 64, 96, 128, 192, 256)
 
 
 class DecodeGraphs:
-    """``model(input_ids [1, n], positions [1, n], batch: PagedBatch) -> logits
-    [n, 1, vocab]`` captured per bucket n."""
+    """Decode steps of ``model(input_ids [1, n], positions [1, n], batch) -> logits
+    [n, 1, vocab]`` as one graph per batch bucket n.
+
+    Step metadata lives in one int32 device block laid out as
+    ``[ctx (M) | ids (M) | positions (M) | tables (M, W)]`` for the largest bucket M and
+    table width W, so bucket n's data is the contiguous prefix of 3 M + n W entries. A
+    step fills a pinned host copy of that prefix with numpy and sends it with a single
+    asynchronous copy; the captured graph widens ids and positions to int64, builds the
+    slot mapping on the device (``decode_slots``) and runs the model. Padding rows have
+    context length 1 in the scratch block.
+    """
 
     def __init__(self, model: Callable, cache: PagedKVCache, scratch_block: int,
                  max_batch: int, max_blocks_per_seq: int) -> None:  # fmt: skip
-        self.model, self.cache = model, cache
+        if max_batch < 1 or max_blocks_per_seq < 1:
+            raise ValueError("DecodeGraphs: max_batch and max_blocks_per_seq must be >= 1")
+        self.model, self.cache, self.scratch_block = model, cache, scratch_block
+        self.sizes = sorted({s for s in BUCKETS if s < max_batch} | {max_batch})
+        self.max_width = max_blocks_per_seq
+        top, w = self.sizes[-1], max_blocks_per_seq
         dev = cache.k.device
-        self.sizes = [s for s in BUCKETS if s < max_batch] + [max_batch]
-        b, w = self.sizes[-1], max_blocks_per_seq
-        self.max_width = w
-        self.scratch_block = scratch_block
-        self.ids = torch.zeros(1, b, dtype=torch.long, device=dev)
-        self.pos = torch.zeros(1, b, dtype=torch.long, device=dev)
-        self.tables = torch.full((b, w), scratch_block, dtype=torch.int32, device=dev)
-        self.ctx = torch.ones(b, dtype=torch.int32, device=dev)
-        self.slots = torch.zeros(b, dtype=torch.int64, device=dev)  # written in-graph
-        self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
-        self.outputs: dict[int, torch.Tensor] = {}
-        self._batches: dict[int, PagedBatch] = {}
-        self._capture()
-
-    def _batch(self, n: int) -> PagedBatch:
-        return PagedBatch(cache=self.cache, slot_mapping=self.slots[:n],
-                          last_index=torch.arange(n, device=self.ids.device),
-                          block_tables=self.tables[:n], context_lens=self.ctx[:n])  # fmt: skip
-
-    def _step(self, n: int, batch: PagedBatch) -> torch.Tensor:
-        decode_slots(self.tables[:n], self.ctx[:n], self.cache.block_size,
-                     self.cache.k.shape[1], out=self.slots[:n])  # fmt: skip
-        return self.model(self.ids[:, :n], self.pos[:, :n], batch)
-
-    def _capture(self) -> None:
-        pool = None
-        for n in reversed(self.sizes):  # largest first: smaller graphs reuse its pool
-            batch = self._batch(n)
-            side = torch.cuda.Stream()
-            side.wait_stream(torch.cuda.current_stream())
-            with torch.cuda.stream(side):
-                for _ in range(2):  # warm-up outside the capture
-                    self._step(n, batch)
-            torch.cuda.current_stream().wait_stream(side)
+        self._host = torch.zeros(3 * top + top * w, dtype=torch.int32, pin_memory=True)
+        self._meta = torch.zeros_like(self._host, device=dev)
+        h = self._host.numpy()
+        self._h_ctx, self._h_ids, self._h_pos = h[:top], h[top : 2 * top], h[2 * top : 3 * top]
+        self._h_tab = h[3 * top :].reshape(top, w)
+        self._ctx, self._ids = self._meta[:top], self._meta[top : 2 * top]
+        self._pos, self._tab = self._meta[2 * top : 3 * top], self._meta[3 * top :].view(top, w)
+        self._slots = torch.empty(top, dtype=torch.int64, device=dev)
+        self._sent = torch.cuda.Event()  # the host block may be rewritten once this fires
+        self._sent.record()
+        self._graphs: dict[int, torch.cuda.CUDAGraph] = {}
+        self._logits: dict[int, torch.Tensor] = {}
+        self._batches = {n: self._batch_of(n) for n in self.sizes}
+        self._stage(top, [], [], [], [])  # an all-padding step for the warm-up
+        self._meta.copy_(self._host)
+        pool = torch.cuda.graph_pool_handle()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):  # warm-up outside any capture: libraries pick kernels
+            for n in self.sizes:
+                self._forward(n)
+        torch.cuda.current_stream().wait_stream(side)
+        for n in self.sizes:
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph, pool=pool):
-                out = self._step(n, batch)
-            pool = graph.pool()
-            # The graph reads the batch's tensors by address: keep them alive.
-            self.graphs[n], self.outputs[n], self._batches[n] = graph, out, batch
+                self._logits[n] = self._forward(n)
+            self._graphs[n] = graph
         torch.cuda.synchronize()
+
+    def _batch_of(self, n: int) -> PagedBatch:
+        """The decode batch of bucket n, all of whose tensors are views of the static
+        buffers (the graph reads them by address)."""
+        flat = torch.arange(n, device=self._meta.device)
+        return PagedBatch(cache=self.cache, slot_mapping=self._slots[:n], kv_slots=flat,
+                          q_index=flat[:, None], q_valid=torch.ones_like(flat[:, None], dtype=torch.bool),
+                          attn_mask=None, last_index=flat, use_kernel=True,
+                          block_tables=self._tab[:n], context_lens=self._ctx[:n])  # fmt: skip
+
+    def _forward(self, n: int) -> torch.Tensor:
+        batch = self._batches[n]
+        decode_slots(batch.block_tables, batch.context_lens, self.cache.block_size,
+                     self.cache.k.shape[1], out=batch.slot_mapping)  # fmt: skip
+        ids = self._ids[:n].to(torch.int64)[None]
+        pos = self._pos[:n].to(torch.int64)[None]
+        return self.model(ids, pos, batch)
+
+    def _stage(self, n: int, ids, positions, tables, context_lens) -> None:
+        """Write bucket n's metadata into the pinned host block (after the previous
+        step's copy has left it)."""
+        self._sent.synchronize()
+        b = len(ids)
+        self._h_ctx[:n] = 1
+        self._h_ctx[:b] = context_lens
+        self._h_ids[:n] = 0
+        self._h_ids[:b] = ids
+        self._h_pos[:n] = 0
+        self._h_pos[:b] = positions
+        self._h_tab[b:n, 0] = self.scratch_block
+        for r, row in enumerate(tables):
+            self._h_tab[r, : len(row)] = row
 
     def can_run(self, batch_size: int, width: int) -> bool:
         return batch_size <= self.sizes[-1] and width <= self.max_width
@@ -82,23 +112,23 @@ class DecodeGraphs:
     def run(self, ids: Sequence[int], positions: Sequence[int], slots: Sequence[int] | None,
             tables: Sequence[Sequence[int]], context_lens: Sequence[int]) -> torch.Tensor:  # fmt: skip
         """One decode step for len(ids) sequences -> logits [B, 1, vocab]. ``slots`` is
-        accepted for the reference's call signature and not used: the captured step
-        builds the slot mapping on the device."""
+        accepted for the reference's signature and ignored: the graph derives them from
+        the tables and lengths."""
         del slots
         b = len(ids)
-        n = next(s for s in self.sizes if s >= b)
-        pad = n - b
+        if not 1 <= b <= self.sizes[-1]:
+            raise ValueError(f"DecodeGraphs: batch {b} outside 1..{self.sizes[-1]}")
         width = max(len(t) for t in tables)
         if width > self.max_width:
             raise ValueError(f"DecodeGraphs: table width {width} > {self.max_width}")
-        rows = [list(t) + [self.scratch_block] * (width - len(t)) for t in tables]
-        rows += [[self.scratch_block] * width] * pad
-        self.ids[0, :n].copy_(torch.tensor(list(ids) + [0] * pad), non_blocking=True)
-        self.pos[0, :n].copy_(torch.tensor(list(positions) + [0] * pad), non_blocking=True)
-        self.ctx[:n].copy_(torch.tensor(list(context_lens) + [1] * pad, dtype=torch.int32))
-        self.tables[:n, :width].copy_(torch.tensor(rows, dtype=torch.int32))
-        self.graphs[n].replay()
-        return self.outputs[n][:b]
+        n = self.sizes[bisect.bisect_left(self.sizes, b)]
+        self._stage(n, np.asarray(ids), np.asarray(positions), tables, np.asarray(context_lens))
+        top = self.sizes[-1]
+        used = 3 * top + n * self.max_width
+        self._meta[:used].copy_(self._host[:used], non_blocking=True)
+        self._sent.record()
+        self._graphs[n].replay()
+        return self._logits[n][:b]
 
 
 # Mixed steps (some sequences reading prompt tokens) by total tokens in the step.
@@ -122,15 +152,20 @@ class MixedGraphs:
     row n - 1, a padding row, so whatever they compute lands there; padding chunks have
     no tokens. Every op outside attention treats rows independently, so real rows
     compute exactly what they would in an eager step.
+
+    ``max_blocks_per_seq`` (table width of the static buffers) defaults to the pool's
+    block count, which holds any table.
     """
 
     def __init__(self, model: Callable, cache: PagedKVCache, scratch_block: int,
-                 max_seqs: int, max_tokens: int, max_blocks_per_seq: int) -> None:  # fmt: skip
+                 max_seqs: int, max_tokens: int,
+                 max_blocks_per_seq: int | None = None) -> None:  # fmt: skip
         self.model, self.cache = model, cache
         dev = cache.k.device
         cap = min(max_tokens + 1, TOKEN_BUCKETS[-1])
         self.sizes = [s for s in TOKEN_BUCKETS if s < cap] + [cap]
-        t, b, w = self.sizes[-1], max_seqs, max_blocks_per_seq
+        w = max_blocks_per_seq or cache.num_blocks
+        t, b = self.sizes[-1], max_seqs
         self.max_seqs, self.max_width = b, w
         self.scratch_block = scratch_block
         self.scratch_slot = scratch_block * cache.block_size
@@ -146,20 +181,20 @@ class MixedGraphs:
         self.ch_tables = torch.full((b, w), scratch_block, dtype=i32, device=dev)
         self.ch_ctx = torch.zeros(b, dtype=i32, device=dev)
         self.cu_q = torch.zeros(b + 1, dtype=i32, device=dev)
-        self.row_tables = torch.full((t, w), scratch_block, dtype=i32, device=dev)
-        self.row_ctx = torch.ones(t, dtype=i32, device=dev)
         self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
         self.outputs: dict[int, torch.Tensor] = {}
         self._batches: dict[int, PagedBatch] = {}
         self._capture()
 
     def _batch(self, n: int) -> PagedBatch:
+        empty = torch.zeros(0, dtype=torch.int64, device=self.ids.device)
         return PagedBatch(
-            cache=self.cache, slot_mapping=self.slots[:n], last_index=self.last, mixed=True,
-            decode_rows=self.dec_rows, block_tables=self.dec_tables, context_lens=self.dec_ctx,
+            cache=self.cache, slot_mapping=self.slots[:n], kv_slots=empty, q_index=empty,
+            q_valid=torch.zeros(0, dtype=torch.bool, device=self.ids.device), attn_mask=None,
+            last_index=self.last, use_kernel=False, mixed=True, decode_rows=self.dec_rows,
+            block_tables=self.dec_tables, context_lens=self.dec_ctx, chunks=[],
             chunk_rows=self.ch_rows[:n], chunk_tables=self.ch_tables, chunk_ctx=self.ch_ctx,
-            cu_seqlens_q=self.cu_q, max_query_len=n, row_tables=self.row_tables[:n],
-            row_ctx=self.row_ctx[:n])  # fmt: skip
+            cu_seqlens_q=self.cu_q, max_query_len=n)  # fmt: skip
 
     def _reset(self, n: int) -> None:
         """Every metadata buffer to its padding value for bucket n (an all-padding step)."""
@@ -174,8 +209,6 @@ class MixedGraphs:
         self.ch_tables.fill_(self.scratch_block)
         self.ch_ctx.zero_()
         self.cu_q.zero_()
-        self.row_tables.fill_(self.scratch_block)
-        self.row_ctx.fill_(1)
 
     def _capture(self) -> None:
         pool = None
@@ -195,9 +228,9 @@ class MixedGraphs:
             self.graphs[n], self.outputs[n], self._batches[n] = graph, out, batch
         torch.cuda.synchronize()
 
-    def can_run(self, num_tokens: int, num_seqs: int, width: int) -> bool:
+    def can_run(self, num_tokens: int, num_seqs: int, width: int | None = None) -> bool:
         return (num_tokens < self.sizes[-1] and num_seqs <= self.max_seqs
-                and width <= self.max_width)  # fmt: skip
+                and (width is None or width <= self.max_width))  # fmt: skip
 
     def run(self, ids: Sequence[int], positions: Sequence[int],
             batch: PagedBatch) -> torch.Tensor:  # fmt: skip
@@ -210,7 +243,7 @@ class MixedGraphs:
         self.pos[0, :t].copy_(torch.tensor(list(positions)), non_blocking=True)
         self.slots[:t].copy_(batch.slot_mapping)
         self.last[:b].copy_(batch.last_index)
-        if batch.decode_rows is not None:
+        if batch.block_tables is not None:
             d, w = batch.block_tables.shape
             self.dec_rows[:d].copy_(batch.decode_rows)
             self.dec_tables[:d, :w].copy_(batch.block_tables)
@@ -223,7 +256,5 @@ class MixedGraphs:
             self.ch_ctx[:c].copy_(batch.chunk_ctx)
             self.cu_q[: c + 1].copy_(batch.cu_seqlens_q)
             self.cu_q[c + 1 :].fill_(tq)  # padding chunks: empty
-            self.row_tables[:tq, :w].copy_(batch.row_tables)
-            self.row_ctx[:tq].copy_(batch.row_ctx)
         self.graphs[n].replay()
         return self.outputs[n][:b]

@@ -173,36 +173,51 @@ def decode_slots(block_tables: torch.Tensor, context_lens: torch.Tensor, block_s
 
 @dataclass
 class PagedBatch:
-    """Everything attention needs for one step, built once and shared by all layers
-    (reference engine/runtime/paged_cache.py:52-229, same role and field names where the
-    meaning is the same). A step's new tokens from every sequence are flattened into one
-    row of N tokens; sequence i owns the next query_lens[i] of them.
+    """Everything attention needs for one step, built once and shared by all layers.
 
-    Decode steps (every sequence adds one token) read K/V through ``block_tables`` /
-    ``context_lens`` in the decode kernel. Mixed steps send sequences adding one token
-    (``decode_rows``) to the decode kernel and every longer run of new tokens -- a
-    prompt or a prompt chunk, its queries last in its context -- to the chunked-prefill
-    kernel through ``chunk_*``. Nothing is gathered.
+    The fields and their meaning are the reference's (engine/runtime/paged_cache.py:52-77),
+    so its unchanged call sites -- ``Attention._paged`` (engine/model/layers.py:191-225),
+    which tests ``use_kernel``, then ``mixed``, else gathers; ``Attention._mixed``
+    (:227-266), which sends decode rows to the decode kernel, then ``varlen``, then loops
+    over ``chunks`` -- dispatch these batches as they dispatch the reference's:
+
+    * decode steps (every sequence adds one token): ``use_kernel`` True,
+      ``block_tables`` / ``context_lens`` for the decode kernel;
+    * mixed steps: ``use_kernel`` False, ``mixed`` True, the decode rows as above, and
+      every longer run of new tokens (a prompt or prompt chunk, its queries last in its
+      context) described for the chunked-prefill kernel by the ``chunk_*`` fields. The
+      reference's ``varlen`` (gathered slots for FlashAttention) is None and ``chunks``
+      (one SDPA per chunk) is empty, so the only line of ``_mixed`` that changes is the
+      varlen call (layers.py:246-253), which becomes ``paged_prefill_attention`` over
+      the ``chunk_*`` fields, for every dtype and head size;
+    * ``use_kernel=False`` builds: the reference's gather metadata (``kv_slots``,
+      ``q_index``, ``q_valid``, ``attn_mask``) for its PyTorch path; this build's call
+      site (engine.model.layers.paged_attention) rejects them.
+
+    A step's new tokens from every sequence are flattened into one row of N tokens;
+    sequence i owns the next query_lens[i] of them.
     """
 
     cache: PagedKVCache
     slot_mapping: torch.Tensor  # [N] int64: where each new token's K/V is written
+    kv_slots: torch.Tensor  # [B, max_ctx] slot of every context position (gather path)
+    q_index: torch.Tensor  # [B, max_q] flat token index of each padded query (gather path)
+    q_valid: torch.Tensor  # [B, max_q] bool (gather path)
+    attn_mask: torch.Tensor | None  # [B, 1, max_q, max_ctx] bool (gather path)
     last_index: torch.Tensor  # [B] flat index of each sequence's last new token
-    use_kernel: bool = True
-    block_tables: torch.Tensor | None = None  # [Bd, W] int32, decode rows
+    use_kernel: bool = False
+    block_tables: torch.Tensor | None = None  # [Bd, W] int32: decode rows
     context_lens: torch.Tensor | None = None  # [Bd] int32, new token included
     mixed: bool = False
     decode_rows: torch.Tensor | None = None  # [Bd] int64 flat token index
+    chunks: list | None = None  # the reference's per-chunk SDPA list: always empty here
+    varlen: tuple | None = None  # the reference's FlashAttention varlen inputs: None here
+    # Chunked-prefill kernel inputs of a mixed step (None without prompt chunks):
     chunk_rows: torch.Tensor | None = None  # [Tq] int64 flat index of every chunk token
     chunk_tables: torch.Tensor | None = None  # [C, W] int32
     chunk_ctx: torch.Tensor | None = None  # [C] int32 context incl. the chunk's tokens
     cu_seqlens_q: torch.Tensor | None = None  # [C + 1] int32 offsets into chunk_rows
     max_query_len: int = 0
-    # Per chunk token, for shapes the chunk kernel does not take (fp32, head_dim 16): the
-    # chunk's table row and the context that token sees (causal), for the decode kernel.
-    row_tables: torch.Tensor | None = None  # [Tq, W] int32
-    row_ctx: torch.Tensor | None = None  # [Tq] int32
-    copy_pairs: torch.Tensor | None = None  # [n, 2] int64 (src, dst) copy-on-write
     # Decode steps with cascade on: the groups of sequences sharing leading blocks
     # (engine.kernels.paged_attention.PrefixGroups), or None.
     prefix_groups: object | None = None
@@ -215,9 +230,9 @@ class PagedBatch:
         context_lens: Sequence[int],
         query_lens: Sequence[int],
         device: str | torch.device,
-        use_kernel: bool = True,
+        use_kernel: bool = False,
         force_mixed: bool = False,
-        copy_pairs: Sequence[tuple[int, int]] = (),
+        *,
         device_slots: bool = False,
         cascade: bool = False,
         num_heads: int | None = None,
@@ -225,21 +240,26 @@ class PagedBatch:
     ) -> PagedBatch:
         """Per sequence, in flattened order: its block table, its context length after
         this step (new tokens included) and its number of new tokens (reference :80-127).
-        ``copy_pairs``: copy-on-write (src, dst) block pairs from the block manager, to
-        apply before this step's writes. ``device_slots``: decode steps compute the slot
+
+        With ``use_kernel``: a step where every sequence adds one token (and not
+        ``force_mixed``) is a decode batch; any other step is a mixed batch -- a single
+        sequence's prompt included, which the reference would gather, since the chunk
+        kernel serves it. Without: the reference's gather metadata.
+        Extensions (keyword-only): ``device_slots``: decode steps compute the slot
         mapping on the device from the uploaded tables instead of on the host.
         ``cascade``: decode steps look for sequences whose tables start with the same
-        blocks (prompt prefixes shared through the prefix cache or a fork; at least
-        ``cascade_min_blocks`` of them, fully covered) and attend to each shared prefix
-        once per group (``paged_decode_attention(prefix_groups=)``); needs the model's
-        ``num_heads``."""
-        if not use_kernel:
-            raise ValueError("PagedBatch: this build has only the kernel path (HIP)")
+        blocks (prompt prefixes shared through a fork; at least ``cascade_min_blocks``
+        of them, fully covered) and attend to each shared prefix once per group
+        (``paged_decode_attention(prefix_groups=)``); needs the model's ``num_heads``.
+        Copy-on-write copies are the caller's, before the step (``cache.copy_blocks``).
+        """
         if not query_lens:
             raise ValueError("PagedBatch: empty step")
-        pairs = None
-        if copy_pairs:
-            pairs = torch.tensor(list(copy_pairs), dtype=torch.int64).view(-1, 2).to(device)
+        if len(block_tables) != len(query_lens) or len(context_lens) != len(query_lens):
+            raise ValueError("PagedBatch: one table, context length and query length per "
+                             "sequence")  # fmt: skip
+        if not use_kernel:
+            return cls._gather(cache, block_tables, context_lens, query_lens, device)
         if max(query_lens) == 1 and not force_mixed:
             batch = cls._decode(cache, block_tables, context_lens, device, device_slots)
             if cascade:
@@ -250,21 +270,62 @@ class PagedBatch:
                 batch.prefix_groups = find_prefix_groups(
                     cls._tables(block_tables), list(context_lens), cache.block_size,
                     num_heads, cache.k.shape[2], device, min_blocks=cascade_min_blocks)  # fmt: skip
-        else:
-            batch = cls._mixed(cache, block_tables, context_lens, query_lens, device)
-        batch.copy_pairs = pairs
-        return batch
+            return batch
+        return cls._mixed(cache, block_tables, context_lens, query_lens, device)
 
     @staticmethod
     def _tables(rows: Sequence[Sequence[int]]) -> torch.Tensor:
         width = max(1, max(len(t) for t in rows))
         return torch.tensor([list(t) + [0] * (width - len(t)) for t in rows], dtype=torch.int32)
 
+    @staticmethod
+    def _check(table: Sequence[int], ctx: int, q: int, bs: int) -> None:
+        if q < 1 or ctx < q:
+            raise ValueError(f"PagedBatch: {q} new tokens in a context of {ctx}")
+        if -(-ctx // bs) > len(table):
+            raise ValueError(f"PagedBatch: a table of {len(table)} blocks cannot hold "
+                             f"{ctx} tokens")  # fmt: skip
+
+    @classmethod
+    def _gather(cls, cache: PagedKVCache, block_tables, context_lens, query_lens,
+                device) -> PagedBatch:  # fmt: skip
+        """The reference's metadata for its PyTorch gather path (reference :100-127):
+        every context slot, padded query indices, and the bottom-right causal mask
+        (query i of a sequence with q new tokens in a context of n sees keys up to
+        n - q + i; padded query rows see key 0 only, so no row is all masked)."""
+        bs = cache.block_size
+        b, max_q, max_ctx = len(query_lens), max(query_lens), max(context_lens)
+        kv = torch.zeros(b, max_ctx, dtype=torch.int64)
+        slot_mapping: list[int] = []
+        for i, (table, ctx, q) in enumerate(zip(block_tables, context_lens, query_lens,
+                                                strict=True)):  # fmt: skip
+            cls._check(table, ctx, q, bs)
+            pos = torch.arange(ctx)
+            kv[i, :ctx] = torch.tensor(list(table), dtype=torch.int64)[pos // bs] * bs + pos % bs
+            slot_mapping += kv[i, ctx - q : ctx].tolist()
+        qlens = torch.tensor(list(query_lens))
+        ctxs = torch.tensor(list(context_lens))
+        starts = torch.cumsum(qlens, 0) - qlens
+        col = torch.arange(max_q)
+        q_valid = col[None] < qlens[:, None]
+        q_index = torch.where(q_valid, starts[:, None] + col[None], 0)
+        q_pos = (ctxs - qlens)[:, None] + col[None]  # [B, max_q] absolute query positions
+        k_pos = torch.arange(max_ctx)
+        see = (k_pos[None, None] <= q_pos[:, :, None]) & (k_pos[None] < ctxs[:, None])[:, None]
+        see |= ~q_valid[:, :, None] & (k_pos == 0)[None, None]
+        return cls(cache=cache,
+                   slot_mapping=torch.tensor(slot_mapping, dtype=torch.int64, device=device),
+                   kv_slots=kv.to(device), q_index=q_index.to(device),
+                   q_valid=q_valid.to(device), attn_mask=see[:, None].to(device),
+                   last_index=(starts + qlens - 1).to(device))  # fmt: skip
+
     @classmethod
     def _decode(cls, cache: PagedKVCache, block_tables, context_lens, device,
                 device_slots: bool) -> PagedBatch:  # fmt: skip
         """Reference :130-156: tables padded with block 0, the new token's slot."""
         bs, b = cache.block_size, len(context_lens)
+        for table, ctx in zip(block_tables, context_lens, strict=True):
+            cls._check(table, ctx, 1, bs)
         tables = cls._tables(block_tables).to(device)
         ctx = torch.tensor(list(context_lens), dtype=torch.int32, device=device)
         if device_slots:
@@ -275,7 +336,9 @@ class PagedBatch:
                  for t, n in zip(block_tables, context_lens, strict=True)],
                 dtype=torch.int64, device=device)  # fmt: skip
         flat = torch.arange(b, device=device)
-        return cls(cache=cache, slot_mapping=slots, last_index=flat, block_tables=tables,
+        return cls(cache=cache, slot_mapping=slots, kv_slots=flat, q_index=flat[:, None],
+                   q_valid=torch.ones(b, 1, dtype=torch.bool, device=device), attn_mask=None,
+                   last_index=flat, use_kernel=True, block_tables=tables,
                    context_lens=ctx)  # fmt: skip
 
     @classmethod
@@ -290,11 +353,7 @@ class PagedBatch:
         ch_rows, ch_tables, ch_ctx, ch_q = [], [], [], []
         start = 0
         for table, ctx, q in zip(block_tables, context_lens, query_lens, strict=True):
-            if q < 1 or ctx < q:
-                raise ValueError(f"PagedBatch: {q} new tokens in a context of {ctx}")
-            if -(-ctx // bs) > len(table):
-                raise ValueError(f"PagedBatch: a table of {len(table)} blocks cannot hold "
-                                 f"{ctx} tokens")  # fmt: skip
+            cls._check(table, ctx, q, bs)
             slots.extend(table[p // bs] * bs + p % bs for p in range(ctx - q, ctx))
             if q == 1:
                 dec_rows.append(start)
@@ -307,26 +366,23 @@ class PagedBatch:
                 ch_q.append(q)
             start += q
         qlens = torch.tensor(list(query_lens), device=device)
-        last = torch.cumsum(qlens, 0) - 1
+        empty = torch.zeros(0, dtype=torch.int64, device=device)
         batch = cls(cache=cache,
                     slot_mapping=torch.tensor(slots, dtype=torch.int64, device=device),
-                    last_index=last, mixed=True)  # fmt: skip
+                    kv_slots=empty, q_index=empty,
+                    q_valid=torch.zeros(0, dtype=torch.bool, device=device), attn_mask=None,
+                    last_index=torch.cumsum(qlens, 0) - 1, use_kernel=False, mixed=True,
+                    decode_rows=torch.tensor(dec_rows, dtype=torch.int64, device=device),
+                    chunks=[])  # fmt: skip
         if dec_rows:
-            batch.decode_rows = torch.tensor(dec_rows, dtype=torch.int64, device=device)
             batch.block_tables = cls._tables(dec_tables).to(device)
             batch.context_lens = torch.tensor(dec_ctx, dtype=torch.int32, device=device)
         if ch_rows:
-            tables = cls._tables(ch_tables)
             cu = torch.zeros(len(ch_q) + 1, dtype=torch.int32)
             cu[1:] = torch.cumsum(torch.tensor(ch_q, dtype=torch.int32), 0)
             batch.chunk_rows = torch.tensor(ch_rows, dtype=torch.int64, device=device)
-            batch.chunk_tables = tables.to(device)
+            batch.chunk_tables = cls._tables(ch_tables).to(device)
             batch.chunk_ctx = torch.tensor(ch_ctx, dtype=torch.int32, device=device)
             batch.cu_seqlens_q = cu.to(device)
             batch.max_query_len = max(ch_q)
-            owner = torch.repeat_interleave(torch.arange(len(ch_q)), torch.tensor(ch_q))
-            within = torch.cat([torch.arange(q) for q in ch_q])
-            batch.row_tables = tables[owner].to(device)
-            batch.row_ctx = (torch.tensor(ch_ctx)[owner] - torch.tensor(ch_q)[owner]
-                             + within + 1).to(torch.int32).to(device)  # fmt: skip
         return batch

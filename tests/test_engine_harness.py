@@ -60,8 +60,10 @@ def test_paged_batch_metadata_matches_definitions():
     tables = [[3, 9, 1], [0], [5, 6, 7, 8], [2, 4]]
     ctx = [10, 1, 13, 6]
     qlen = [1, 1, 5, 6]  # two decode rows, a later chunk, a whole prompt
-    b = PagedBatch.build(cache, tables, ctx, qlen, "cpu")
-    assert b.mixed
+    b = PagedBatch.build(cache, tables, ctx, qlen, "cpu", use_kernel=True)
+    # The reference's dispatch (layers.py:200-212) tests use_kernel before mixed:
+    # mixed batches must not claim the decode kernel; chunks stay empty, varlen None.
+    assert b.mixed and not b.use_kernel and b.chunks == [] and b.varlen is None
     want_slots = [t[p // 4] * 4 + p % 4 for t, n, q in zip(tables, ctx, qlen)
                   for p in range(n - q, n)]  # fmt: skip
     assert b.slot_mapping.tolist() == want_slots
@@ -71,16 +73,42 @@ def test_paged_batch_metadata_matches_definitions():
     assert b.chunk_rows.tolist() == list(range(2, 13))
     assert b.cu_seqlens_q.tolist() == [0, 5, 11] and b.max_query_len == 6
     assert b.chunk_ctx.tolist() == [13, 6]
-    # Query i of a chunk of q tokens in a context of n sees keys 0 .. n - q + i.
-    assert b.row_ctx.tolist() == [9, 10, 11, 12, 13, 1, 2, 3, 4, 5, 6]
-    assert b.row_tables[0].tolist() == [5, 6, 7, 8] and b.row_tables[5].tolist()[:2] == [2, 4]
-    d = PagedBatch.build(cache, tables[:2], ctx[:2], [1, 1], "cpu")
-    assert not d.mixed and d.slot_mapping.tolist() == want_slots[:2]
+    assert b.chunk_tables[0].tolist() == [5, 6, 7, 8] and b.chunk_tables[1].tolist()[:2] == [2, 4]
+    d = PagedBatch.build(cache, tables[:2], ctx[:2], [1, 1], "cpu", use_kernel=True)
+    assert d.use_kernel and not d.mixed and d.slot_mapping.tolist() == want_slots[:2]
     assert d.block_tables.tolist() == [[3, 9, 1], [0, 0, 0]]  # padded with block 0
+    # One sequence's prompt with the kernel: a mixed batch (the chunk kernel takes it).
+    one = PagedBatch.build(cache, tables[2:3], ctx[2:3], qlen[2:3], "cpu", use_kernel=True)
+    assert one.mixed and not one.use_kernel and one.block_tables is None
+    assert one.chunk_rows.tolist() == list(range(5)) and one.decode_rows.numel() == 0
     with pytest.raises(ValueError):
-        PagedBatch.build(cache, [[1]], [9], [2], "cpu")  # table too short
-    with pytest.raises(ValueError):
-        PagedBatch.build(cache, [[1]], [2], [1], "cpu", use_kernel=False)
+        PagedBatch.build(cache, [[1]], [9], [2], "cpu", use_kernel=True)  # table too short
+
+
+def test_paged_batch_gather_metadata_matches_definitions():
+    """use_kernel=False: the reference's gather metadata (paged_cache.py:100-127) --
+    every context slot, padded query indices and the bottom-right causal mask."""
+    cfg = TinyConfig()
+    cache = PagedKVCache(cfg, 40, 4, "cpu", torch.float32)
+    tables = [[3, 9, 1], [5, 6, 7, 8]]
+    ctx, qlen = [10, 13], [1, 5]
+    g = PagedBatch.build(cache, tables, ctx, qlen, "cpu")
+    assert not g.use_kernel and not g.mixed
+    for i, (t, n) in enumerate(zip(tables, ctx)):
+        assert g.kv_slots[i, :n].tolist() == [t[p // 4] * 4 + p % 4 for p in range(n)]
+    assert g.slot_mapping.tolist() == [g.kv_slots[0, 9].item()] + g.kv_slots[1, 8:13].tolist()
+    assert g.q_valid.tolist() == [[True] + [False] * 4, [True] * 5]
+    assert g.q_index.tolist() == [[0, 0, 0, 0, 0], [1, 2, 3, 4, 5]]
+    assert g.last_index.tolist() == [0, 5]
+    m = g.attn_mask[:, 0]
+    assert m.shape == (2, 5, 13)
+    assert m[0, 0].tolist() == [True] * 10 + [False] * 3  # decode row: its whole context
+    # Padded query rows: keys k <= n - q + i inside the context, plus key 0 always.
+    for i in range(1, 5):
+        assert m[0, i].tolist() == [(k <= 9 + i and k < 10) or k == 0 for k in range(13)]
+    assert m[1].any(-1).all()  # no row is fully masked
+    for i in range(5):  # query i of the chunk sits at 8 + i
+        assert m[1, i].tolist() == [k <= 8 + i for k in range(13)]
 
 
 def test_paged_batch_cascade_groups():
@@ -90,16 +118,18 @@ def test_paged_batch_cascade_groups():
     cache = PagedKVCache(cfg, 32, 4, "cpu", torch.float32)
     shared = [1, 2, 3]
     tables = [shared + [10, 11], shared + [12], [20, 21, 22, 23]]
-    b = PagedBatch.build(cache, tables, [18, 14, 15], [1, 1, 1], "cpu", cascade=True,
-                         num_heads=cfg.num_attention_heads, cascade_min_blocks=2)  # fmt: skip
+    b = PagedBatch.build(cache, tables, [18, 14, 15], [1, 1, 1], "cpu", use_kernel=True,
+                         cascade=True, num_heads=cfg.num_attention_heads,
+                         cascade_min_blocks=2)  # fmt: skip
     pg = b.prefix_groups
     assert pg is not None and pg.members == 2
     assert pg.first_block.tolist() == [3, 3, 0] and pg.prefix_row.tolist()[2] == -1
-    none = PagedBatch.build(cache, tables[2:], [15], [1], "cpu", cascade=True,
+    none = PagedBatch.build(cache, tables[2:], [15], [1], "cpu", use_kernel=True, cascade=True,
                             num_heads=cfg.num_attention_heads, cascade_min_blocks=2)  # fmt: skip
     assert none.prefix_groups is None
     with pytest.raises(ValueError):
-        PagedBatch.build(cache, tables, [18, 14, 15], [1, 1, 1], "cpu", cascade=True)
+        PagedBatch.build(cache, tables, [18, 14, 15], [1, 1, 1], "cpu", use_kernel=True,
+                         cascade=True)
 
 
 @pytest.mark.parametrize("budget", [4096, 8])
@@ -112,8 +142,8 @@ def test_engine_reference_backend_matches_static_loop(budget):
     _check_logits(eng, PROMPTS, 10, atol=1e-4)
     assert any(not s["decode_only"] for s in eng.log) and any(s["decode_only"] for s in eng.log)
     assert eng.bm.num_free_blocks == 64
-    # Prefix-cache hits happened ("b", "d", "f" share 12 tokens).
-    assert eng.bm.num_cached_blocks > 0
+    # Prompts "b", "d", "f" share 12 tokens: later ones forked the first one's blocks.
+    assert eng.prefix_hits > 0
 
 
 def test_engine_fork_copy_on_write_reference_backend():
@@ -159,8 +189,8 @@ def _cuda_model(dtype, **cfg):
 @pytest.mark.gpu
 @pytest.mark.parametrize("budget", [4096, 8])
 def test_engine_kernels_match_static_loop_fp32(budget):
-    """fp32: decode kernel (fp32 instantiation) and, for prompt chunks, the decode kernel
-    per chunk token. Tokens and logits == the static loop."""
+    """fp32: decode kernel (fp32 instantiation) and, for prompt chunks, the VALU
+    chunked-prefill kernel. Tokens and logits == the static loop."""
     from tiny_llama import KernelBackend
 
     model = _cuda_model(torch.float32)
@@ -169,7 +199,7 @@ def test_engine_kernels_match_static_loop_fp32(budget):
                      max_num_batched_tokens=budget)  # fmt: skip
     assert _run_staggered(eng, PROMPTS, 10) == want
     _check_logits(eng, PROMPTS, 10, atol=2e-4)
-    assert eng.bm.num_free_blocks == 64 and eng.bm.num_cached_blocks > 0
+    assert eng.bm.num_free_blocks == 64 and eng.prefix_hits > 0
 
 
 @pytest.mark.gpu
@@ -198,7 +228,7 @@ def test_engine_kernels_match_reference_backend_16bit(dtype, hd, bs):
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_engine_cascade_decode_matches_plain(dtype):
-    """Decode steps with cascade over prompt prefixes shared through the prefix cache:
+    """Decode steps with cascade over prompt prefixes shared by forking blocks:
     the plain decode's tokens, logits within 16-bit rounding."""
     from tiny_llama import KernelBackend
 
@@ -271,7 +301,7 @@ def test_engine_fork_copy_on_write_kernels(graphs):
 @pytest.mark.parametrize("budget", [4096, 8])
 def test_mixed_graphs_match_eager(dtype, budget):
     """Mixed steps replayed as one hipGraph per token bucket (prompts joining while
-    others decode, chunked under budget 8, prefix-cache hits) give the eager engine's
+    others decode, chunked under budget 8, shared prompt prefixes) give the eager engine's
     tokens; in fp32 also the static loop's. Decode-only steps use DecodeGraphs."""
     from tiny_llama import KernelBackend
 

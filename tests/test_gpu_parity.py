@@ -160,25 +160,6 @@ def test_copy_blocks_bit_exact(bs, nkv, hd, dtype):
     assert torch.equal(_bits(cache.k.cpu()), _bits(kc)) and torch.equal(_bits(cache.v.cpu()), _bits(vc))
 
 
-def test_copy_blocks_config3_cow():
-    """Config 3's copy-on-write: 64 copies of the last shared block, then decode parity."""
-    _say("config3 CoW + decode")
-    step = workloads.config3(DEV, seed=0)
-    before = step.k_cache.clone()
-    copy_blocks(step.k_cache, step.v_cache, step.cow_mapping, step.block_size)
-    torch.cuda.synchronize()
-    bs = step.block_size
-    for s, d in step.cow_mapping.tolist():
-        assert torch.equal(_bits(step.k_cache[d * bs : (d + 1) * bs]), _bits(before[s * bs : (s + 1) * bs]))
-    kv_append(step.k_cache, step.v_cache, step.new_k, step.new_v, step.slot_mapping)
-    # oracle on a subset of sequences (8 of 256, with and without CoW)
-    idx = torch.tensor([0, 1, 63, 64, 100, 200, 254, 255])
-    sub = workloads.DecodeStep(step.name, step.q[idx], step.k_cache, step.v_cache,
-                               step.block_tables[idx], step.context_lens[idx], bs,
-                               step.new_k, step.new_v, step.slot_mapping)  # fmt: skip
-    _check_attention(sub, what="c3 subset")
-
-
 # ---- decode attention --------------------------------------------------------------------
 
 
@@ -268,42 +249,6 @@ def test_decode_table_row_stride_and_graph_padding_rows():
                                 real.new_k, real.new_v, real.slot_mapping)  # fmt: skip
     assert step.block_tables.stride(0) == 40
     _check_attention(step, what="padded")
-
-
-@pytest.mark.parametrize("name", ["c1", "c2"])
-def test_decode_configs_full(name):
-    """Configs 1 and 2 at full size: append, then decode attention, vs the oracle."""
-    _say("config", name)
-    step = workloads.CONFIGS[name](DEV, seed=0)
-    kc, vc = step.k_cache.cpu(), step.v_cache.cpu()
-    oracle.kv_append(kc, vc, step.new_k.cpu(), step.new_v.cpu(), step.slot_mapping.cpu())
-    kv_append(step.k_cache, step.v_cache, step.new_k, step.new_v, step.slot_mapping)
-    torch.cuda.synchronize()
-    assert torch.equal(_bits(step.k_cache.cpu()), _bits(kc))
-    assert torch.equal(_bits(step.v_cache.cpu()), _bits(vc))
-    _check_attention(step, what=name)
-
-
-def test_decode_config4_long_context():
-    """Config 4 (log-uniform up to 32k tokens): full-size partition invariance, and the
-    oracle on the longest and shortest sequences."""
-    _say("config4")
-    step = workloads.config4(DEV, seed=0)
-    args = (step.q, step.k_cache, step.v_cache, step.block_tables, step.context_lens, 16)
-    outs = []
-    for wgs in (None, 97, 1024):
-        o = torch.empty(step.q.shape, dtype=torch.float32, device=DEV)
-        pa.paged_decode_attention(*args, out=o, num_workgroups=wgs)
-        outs.append(o)
-    torch.cuda.synchronize()
-    for o in outs[1:]:
-        assert (o - outs[0]).abs().max().item() < 1e-5
-    order = step.context_lens.argsort().cpu()
-    idx = torch.cat([order[:2], order[-2:]])
-    sub = workloads.DecodeStep(step.name, step.q[idx], step.k_cache, step.v_cache,
-                               step.block_tables[idx], step.context_lens[idx], 16,
-                               step.new_k, step.new_v, step.slot_mapping)  # fmt: skip
-    _check_attention(sub, what="c4 subset")
 
 
 def test_graph_capture_replay():

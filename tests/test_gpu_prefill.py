@@ -1,5 +1,6 @@
-"""Parity of the MFMA chunked-prefill kernel (through the C ABI) with the CPU oracle's
-bottom-right causal chunk attention (the semantics of the reference's PagedBatch._mixed
+"""Parity of the chunked-prefill kernels (through the C ABI) -- the matrix-core kernel for
+16-bit K/V at head_dim 32-256, the VALU kernel for fp32 and head_dim 16 -- with the CPU
+oracle's bottom-right causal chunk attention (the semantics of the reference's PagedBatch._mixed
 and Attention._mixed, engine/runtime/paged_cache.py:182-194, engine/model/layers.py:
 246-265). The fp32 result must be within max-abs 2e-3 of the oracle; the q.dtype result
 equals that fp32 result rounded by torch."""
@@ -59,17 +60,85 @@ def _run(q, k, v, tables, ctx, cu, bs, max_q):
     return out32.cpu()
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize(("nh", "nkv", "hd"), [(8, 2, 64), (4, 2, 128), (24, 8, 128), (6, 2, 32)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize(("nh", "nkv", "hd"),
+                         [(8, 2, 64), (4, 2, 128), (24, 8, 128), (6, 2, 32), (4, 2, 16)])
 def test_prefill_reference_varlen_spec(dtype, nh, nkv, hd):
-    """The reference's own mixed-step spec (tests/test_kernels.py:199), block size 4."""
+    """The reference's own mixed-step spec (tests/test_kernels.py:199), block size 4; its
+    tiny model's shape (4 q / 2 KV heads, hd 16) included. fp32 also within the
+    reference's fp32 tolerance, 1e-4 (tests/test_kernels.py:36)."""
     _say("prefill varlen spec", dtype, nh, nkv, hd)
     spec = [(1, 9), (6, 6), (1, 3), (5, 13), (3, 20), (1, 1)]
     q, k, v, tables, ctx, cu = _chunks(spec, nh, nkv, hd, 4, dtype, seed=0)
     got = _run(q, k, v, tables, ctx, cu, 4, max(s for s, _ in spec))
     want = oracle.prefill_attention(q, k, v, tables, cu, ctx, 4, threads=THREADS)
     err = (got - want).abs().max().item()
-    assert err <= ATOL, err
+    assert err <= (1e-4 if dtype == torch.float32 else ATOL), err
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize(("nh", "nkv", "hd", "bs"),
+                         [(4, 2, 16, 4), (8, 8, 256, 16), (12, 2, 64, 3), (5, 1, 128, 16),
+                          (8, 1, 32, 8)])  # fmt: skip
+def test_prefill_valu_kernel_shapes(dtype, nh, nkv, hd, bs):
+    """The VALU kernel (fp32 at every head dim, 16-bit at hd 16 only; the bf16 cases at
+    other dims cross-check the matrix-core kernel on the same inputs): multi-tile
+    contexts (64-key tiles, 32 at hd 256), query tiles of 16 tokens cut mid-chunk, groups
+    of 1-12 heads (sub-groups of 4 with masked heads), block sizes that are not powers
+    of two, empty chunks."""
+    _say("prefill valu", dtype, nh, nkv, hd, bs)
+    spec = [(37, 300), (16, 16), (0, 7), (1, 129), (70, 70), (17, 200)]
+    q, k, v, tables, ctx, cu = _chunks(spec, nh, nkv, hd, bs, dtype, seed=hd + nh + bs)
+    got = _run(q, k, v, tables, ctx, cu, bs, 70)
+    want = oracle.prefill_attention(q, k, v, tables, cu, ctx, bs, threads=THREADS)
+    err = (got - want).abs().max().item()
+    assert err <= (1e-4 if dtype == torch.float32 else ATOL), err
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_prefill_valu_non_causal_rows_and_lse(dtype):
+    """pkv_paged_prefill_ex on the VALU kernel: causal = 0 (every query sees the chunk's
+    whole context), queries gathered through q_rows, log2 normalisers. Non-causal
+    attention of one query over n keys is the decode oracle with context n; the
+    normaliser is checked in float64 from its definition."""
+    from engine.kernels import _native
+
+    _say("prefill valu ex", dtype)
+    nh, nkv, hd, bs = 4, 2, 16, 4
+    spec = [(3, 21), (5, 9)]
+    q, k, v, tables, ctx, cu = _chunks(spec, nh, nkv, hd, bs, dtype, seed=11)
+    t = q.shape[0]
+    rows = torch.randperm(t, generator=torch.Generator().manual_seed(1)).int()
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    out = torch.empty(t, nh, hd, dtype=torch.float32, device=DEV)
+    lse = torch.empty(t, nh, dtype=torch.float32, device=DEV)
+    td, cd, cud, rd = tables.to(DEV), ctx.to(DEV), cu.to(DEV), rows.to(DEV)
+    st = _native.lib().pkv_paged_prefill_ex(
+        out.data_ptr(), _native.PKV_F32, out.stride(0), out.stride(1), qd.data_ptr(),
+        qd.stride(0), qd.stride(1), kd.data_ptr(), vd.data_ptr(), _native.dtype_code(dtype, "t"),
+        kd.stride(0), kd.stride(1), kd.shape[0], td.data_ptr(), td.stride(0), td.shape[1],
+        cd.data_ptr(), cud.data_ptr(), len(spec), 5, nh, nkv, hd, bs, hd**-0.5, 0,
+        rd.data_ptr(), lse.data_ptr(), torch.cuda.current_stream().cuda_stream)  # fmt: skip
+    _native.check(st, "prefill_ex")
+    torch.cuda.synchronize()
+    owner = torch.repeat_interleave(torch.arange(len(spec)), torch.tensor([a for a, _ in spec]))
+    row_tables = tables[owner].contiguous()
+    row_ctx = ctx[owner].contiguous()
+    want = oracle.decode_attention(q[rows.long()].contiguous(), k, v, row_tables, row_ctx, bs,
+                                   threads=THREADS)  # fmt: skip
+    err = (out.cpu() - want).abs().max().item()
+    assert err <= (1e-4 if dtype == torch.float32 else ATOL), err
+    g = nh // nkv
+    for i in range(t):
+        n = int(row_ctx[i])
+        pos = torch.arange(n)
+        sl = row_tables[i, pos // bs].long() * bs + pos % bs
+        kk = k[sl].double().repeat_interleave(g, 1)  # [n, nh, hd]
+        sc = (kk * q[rows[i].long()].double()[None]).sum(-1) * hd**-0.5 / torch.log(
+            torch.tensor(2.0, dtype=torch.float64))  # log2 units
+        ref = torch.logsumexp(sc * torch.log(torch.tensor(2.0, dtype=torch.float64)), 0) / \
+            torch.log(torch.tensor(2.0, dtype=torch.float64))  # fmt: skip
+        assert (lse[i].cpu().double() - ref).abs().max().item() <= 1e-4
 
 
 @pytest.mark.parametrize(("nh", "nkv"), [(32, 8), (24, 8), (8, 8), (16, 1)])

@@ -235,15 +235,25 @@ class ReferenceBackend:
         cache.v[layer].index_copy_(0, batch.slot_mapping, v.to(cache.v.dtype))
         kc, vc, bs = cache.k[layer], cache.v[layer], cache.block_size
         out = torch.empty_like(q)
-        if not batch.mixed:
+        if batch.use_kernel:
             return reference_decode_attention(q, kc, vc, batch.block_tables,
                                               batch.context_lens, bs).flatten(1)  # fmt: skip
-        if batch.decode_rows is not None:
+        if batch.block_tables is not None:
             out[batch.decode_rows] = reference_decode_attention(
                 q[batch.decode_rows], kc, vc, batch.block_tables, batch.context_lens, bs)
         if batch.chunk_rows is not None:
+            # Each chunk token as a decode row over its own causal prefix: query i of a
+            # chunk of q tokens in a context of n sees keys 0 .. n - q + i.
+            cu = batch.cu_seqlens_q.tolist()
+            owner, seen = [], []
+            for c, n in enumerate(batch.chunk_ctx.tolist()):
+                ql = cu[c + 1] - cu[c]
+                owner += [c] * ql
+                seen += [n - ql + i + 1 for i in range(ql)]
+            tables = batch.chunk_tables[torch.tensor(owner, device=q.device)]
+            ctx = torch.tensor(seen, dtype=torch.int32, device=q.device)
             out[batch.chunk_rows] = reference_decode_attention(
-                q[batch.chunk_rows], kc, vc, batch.row_tables, batch.row_ctx, bs)
+                q[batch.chunk_rows], kc, vc, tables, ctx, bs)
         return out.flatten(1)
 
     def copy(self, cache: PagedKVCache, pairs: torch.Tensor) -> None:
@@ -269,13 +279,16 @@ class Seq:
 
 class TinyEngine:
     """Each step: running sequences first (a decode token, or the next prompt chunk
-    within the token budget), then waiting ones while seats and budget last, with
-    prefix-cache matching. One extra pool block past the allocator's range is the
-    graph-padding scratch block (reference engine/runtime/engine.py:73-74)."""
+    within the token budget), then waiting ones while seats and budget last. A new
+    prompt that starts with the same full blocks of tokens as a running sequence's
+    computed tokens forks those blocks (``share_prefixes``), so sequences share K/V as
+    the reference's prefix cache makes them do. One extra pool block past the
+    allocator's range is the graph-padding scratch block (reference
+    engine/runtime/engine.py:73-74)."""
 
     def __init__(self, model: TinyLlama, backend, num_blocks: int = 64, block_size: int = 4,
                  max_num_seqs: int = 8, max_num_batched_tokens: int = 4096,
-                 enable_prefix_caching: bool = True, graphs: bool = False,
+                 share_prefixes: bool = True, graphs: bool = False,
                  mixed_graphs: bool = False, debug_checks: bool = True,
                  cascade_min_blocks: int | None = None) -> None:  # fmt: skip
         self.model, self.backend = model, backend
@@ -283,7 +296,9 @@ class TinyEngine:
         self.device, self.dtype = w.device, w.dtype
         cfg = model.cfg
         self.cache = PagedKVCache(cfg, num_blocks + 1, block_size, self.device, self.dtype)
-        self.bm = BlockManager(num_blocks, block_size, enable_prefix_caching)
+        self.bm = BlockManager(num_blocks, block_size)
+        self.share_prefixes = share_prefixes
+        self.prefix_hits = 0  # admitted prompts that forked another sequence's blocks
         self.max_num_seqs, self.budget = max_num_seqs, max_num_batched_tokens
         self.debug_checks = debug_checks
         # eager decode steps: cascade over prefixes of at least this many shared blocks
@@ -306,7 +321,7 @@ class TinyEngine:
             from engine.runtime.cuda_graphs import MixedGraphs
 
             self.mixed_graphs = MixedGraphs(model, self.cache, num_blocks, max_num_seqs,
-                                            max_num_batched_tokens, num_blocks)  # fmt: skip
+                                            max_num_batched_tokens)  # fmt: skip
 
     def add_request(self, rid: str, prompt: list[int], max_tokens: int) -> None:
         self.waiting.append(Seq(rid, self._next_id, list(prompt), len(prompt), max_tokens))
@@ -344,12 +359,33 @@ class TinyEngine:
             if not self.bm.can_grow(seq.seq_id, len(seq.ids)):
                 break
             self.waiting.pop(0)
-            seq.num_computed = self.bm.match_prefix(seq.seq_id, seq.ids)
+            seq.num_computed = self._share_prefix(seq)
             self.running.append(seq)
             n = min(len(seq.ids) - seq.num_computed, budget)
             plan.append((seq, n))
             budget -= n
         return plan
+
+    def _share_prefix(self, seq: Seq) -> int:
+        """Fork the longest run of leading full blocks whose tokens a running sequence has
+        computed and the new prompt starts with (at least one prompt token is left to
+        compute: its logits are needed). Returns the tokens now in place."""
+        if not self.share_prefixes:
+            return 0
+        bs = self.bm.block_size
+        best, donor = 0, None
+        for other in self.running:
+            limit = min(other.num_computed, len(seq.ids) - 1) // bs
+            k = 0
+            while k < limit and other.ids[k * bs : (k + 1) * bs] == seq.ids[k * bs : (k + 1) * bs]:
+                k += 1
+            if k > best:
+                best, donor = k, other
+        if donor is None:
+            return 0
+        self.bm.fork(donor.seq_id, seq.seq_id, num_tokens=best * bs)
+        self.prefix_hits += 1
+        return best * bs
 
     def step(self) -> list[tuple[str, int]]:
         plan = self._schedule()
@@ -376,13 +412,14 @@ class TinyEngine:
             used_graph = True
         elif self.mixed_graphs is not None and not decode_only and \
                 self.mixed_graphs.can_run(len(ids), len(plan), width):  # fmt: skip
-            batch = PagedBatch.build(self.cache, tables, ctx, qlens, self.device)
+            batch = PagedBatch.build(self.cache, tables, ctx, qlens, self.device,
+                                     use_kernel=True, force_mixed=True)  # fmt: skip
             logits = self.mixed_graphs.run(ids, positions, batch)[:, 0]
             used_mixed_graph = True
         else:
             cascade = self.cascade_min_blocks is not None
             batch = PagedBatch.build(self.cache, tables, ctx, qlens, self.device,
-                                     cascade=cascade, num_heads=self.model.cfg.num_attention_heads,
+                                     use_kernel=True, cascade=cascade, num_heads=self.model.cfg.num_attention_heads,
                                      cascade_min_blocks=self.cascade_min_blocks or 16)  # fmt: skip
             logits = self.model(torch.tensor([ids], device=self.device),
                                 torch.tensor([positions], device=self.device), batch)[:, 0]  # fmt: skip
@@ -390,7 +427,6 @@ class TinyEngine:
         outputs = []
         for row, (seq, n) in enumerate(plan):
             seq.num_computed += n
-            self.bm.register_full_blocks(seq.seq_id, seq.ids, seq.num_computed)
             if seq.num_computed < len(seq.ids):
                 continue  # a prompt chunk: nothing to sample yet
             tok = greedy[row]
