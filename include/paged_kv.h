@@ -33,6 +33,10 @@ extern "C" {
 #define PKV_E_WORKSPACE (-4) /* split-K workspace missing or too small */
 #define PKV_E_NULL (-5)      /* required pointer is NULL */
 #define PKV_E_HIP (-6)       /* a HIP device query failed (no usable GPU) */
+#define PKV_E_SCRATCH (-7)   /* the call needs more than the no-alloc scratch holds */
+
+/* Bytes of the static device scratch behind pkv_paged_decode_noalloc (per GPU). */
+#define PKV_NOALLOC_SCRATCH_BYTES (32LL << 20)
 
 /* ABI version, bumped on any signature change. */
 int pkv_abi_version(void);
@@ -125,6 +129,29 @@ int pkv_paged_decode(void* out, int out_dtype, int64_t out_stride_b, int64_t out
                      int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
                      float scale, int32_t num_workgroups, void* workspace,
                      int64_t workspace_bytes, void* stream);
+
+/*
+ * pkv_paged_decode without a workspace argument, for callers that cannot allocate (code
+ * under hipGraph capture that must not call hipMalloc, tight serving loops, harnesses
+ * that forbid allocation). No counterpart in the reference: its Triton decode needs no
+ * scratch. Same arguments, kernels and results as pkv_paged_decode at the same
+ * num_workgroups; the split-K workspace is a static device array of
+ * PKV_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends. Calls whose workspace
+ * (pkv_decode_workspace_bytes) exceeds it return PKV_E_SCRATCH before any launch. The
+ * first call on a device resolves the array's address (make it outside graph capture).
+ * Calls on one GPU share the array: calls that overlap on one GPU (concurrent streams)
+ * race on it and must be serialised by the caller. Nothing is allocated, copied
+ * synchronously or synchronised.
+ */
+int pkv_paged_decode_noalloc(void* out, int out_dtype, int64_t out_stride_b,
+                             int64_t out_stride_h, const void* q, int64_t q_stride_b,
+                             int64_t q_stride_h, const void* k_cache, const void* v_cache,
+                             int kv_dtype, int64_t kv_stride_slot, int64_t kv_stride_head,
+                             int64_t num_slots, const int32_t* block_tables,
+                             int64_t table_stride, int32_t max_blocks,
+                             const int32_t* context_lens, int32_t batch, int32_t num_heads,
+                             int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                             float scale, int32_t num_workgroups, void* stream);
 
 /* Bytes of scratch pkv_paged_decode_ex needs with prefix parts (cascade): the split-K
  * scratch plus fp32 room for the sequences the stream pass finishes, [batch, num_heads,

@@ -3,6 +3,8 @@
 
 #include "common.h"
 
+#include <mutex>
+
 namespace {
 
 using namespace pkv;
@@ -1214,6 +1216,35 @@ int check_decode_shape(int kv_dtype, int head_dim, int num_heads, int num_kv_hea
   return 0;
 }
 
+// Scratch of pkv_paged_decode_noalloc: the decode workspace (merge plans and partial
+// records) for callers that cannot allocate. Each GPU the library runs on holds its own
+// copy until the process ends. Host code must never pass `scratch` itself to a kernel (in
+// host code the name is only a stand-in for the device symbol): it uses the per-device
+// address hipGetSymbolAddress returns, kept in g_scratch_ptr.
+static __device__ __align__(256) unsigned char scratch[PKV_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+void* g_scratch_ptr[kMaxDevices] = {};
+std::mutex g_scratch_mu;
+
+// The current device's address of `scratch`, resolved on the first call per device (with
+// that device current) and cached. Returns 0 or a PKV_E_* / hipError_t status.
+int scratch_address(void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return PKV_E_HIP;
+  if (dev >= kMaxDevices) return PKV_E_SHAPE;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (!p) return PKV_E_HIP;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1360,6 +1391,37 @@ int pkv_paged_decode_ex(void* out, int out_dtype, int64_t out_stride_b, int64_t 
 
   hipStream_t st = (hipStream_t)stream;
   return (int)by_dtype(kv_dtype, head_dim, p.gpw, LaunchDecode{&a, p.wpg, p.ygrid, st});
+}
+
+int pkv_paged_decode_noalloc(void* out, int out_dtype, int64_t out_stride_b,
+                             int64_t out_stride_h, const void* q, int64_t q_stride_b,
+                             int64_t q_stride_h, const void* k_cache, const void* v_cache,
+                             int kv_dtype, int64_t kv_stride_slot, int64_t kv_stride_head,
+                             int64_t num_slots, const int32_t* block_tables,
+                             int64_t table_stride, int32_t max_blocks,
+                             const int32_t* context_lens, int32_t batch, int32_t num_heads,
+                             int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                             float scale, int32_t num_workgroups, void* stream) {
+  const int bad = check_decode_shape(kv_dtype, head_dim, num_heads, num_kv_heads);
+  if (bad) return bad;
+  if (batch < 0 || num_workgroups < 1 || num_workgroups > (1 << 24) || batch > (1 << 24))
+    return PKV_E_SHAPE;
+  // The same workspace layout the allocating entry point asks its caller for; it must
+  // fit the static array (no contents need clearing: every record is written before
+  // the combine reads it, within the call).
+  const int64_t need = decode_ws(num_workgroups, batch, num_heads, head_dim, false).total;
+  if (need > PKV_NOALLOC_SCRATCH_BYTES) return PKV_E_SCRATCH;
+  void* ws = nullptr;
+  if (need > 0 && batch > 0) {
+    const int st = scratch_address(&ws);
+    if (st) return st;
+  }
+  return pkv_paged_decode_ex(out, out_dtype, out_stride_b, out_stride_h, q, q_stride_b,
+                             q_stride_h, k_cache, v_cache, kv_dtype, kv_stride_slot,
+                             kv_stride_head, num_slots, block_tables, table_stride, max_blocks,
+                             context_lens, batch, num_heads, num_kv_heads, head_dim, block_size,
+                             scale, num_workgroups, ws, ws ? PKV_NOALLOC_SCRATCH_BYTES : 0,
+                             nullptr, nullptr, nullptr, nullptr, nullptr, 0, 0, stream);
 }
 
 }  // extern "C"

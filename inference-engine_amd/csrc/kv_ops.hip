@@ -194,7 +194,7 @@ hipError_t append_out(int dout, bool vec, void* kp, void* vp, int64_t ps_slot,
 
 extern "C" {
 
-int pkv_abi_version(void) { return 2; }
+int pkv_abi_version(void) { return 3; }
 
 const char* pkv_status_string(int status) {
   switch (status) {
@@ -205,6 +205,7 @@ const char* pkv_status_string(int status) {
     case PKV_E_WORKSPACE: return "split-K workspace missing or too small";
     case PKV_E_NULL: return "required pointer is NULL";
     case PKV_E_HIP: return "HIP device query failed (no usable GPU?)";
+    case PKV_E_SCRATCH: return "the call needs more scratch than the no-alloc entry point holds";
     default: return status > 0 ? hipGetErrorString((hipError_t)status) : "unknown error";
   }
 }

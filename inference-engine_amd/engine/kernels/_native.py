@@ -18,7 +18,8 @@ LIB_PATH = os.path.join(
     "lib",
     "libpaged_kv.so",
 )
-ABI_VERSION = 2
+ABI_VERSION = 3
+PKV_NOALLOC_SCRATCH_BYTES = 32 << 20  # include/paged_kv.h
 
 PKV_F32, PKV_F16, PKV_BF16 = 0, 1, 2
 DTYPE_CODE = {torch.float32: PKV_F32, torch.float16: PKV_F16, torch.bfloat16: PKV_BF16}
@@ -46,6 +47,15 @@ SIGNATURES: dict[str, tuple] = {
          _p, _i64, _i32,                          # block tables
          _p, _i32, _i32, _i32, _i32, _i32,        # ctx, batch, nh, nkv, hd, bs
          _f32, _i32, _p, _i64, _p],               # scale, wgs, workspace, stream
+    ),  # fmt: skip
+    "pkv_paged_decode_noalloc": (
+        ctypes.c_int,
+        [_p, ctypes.c_int, _i64, _i64,            # out
+         _p, _i64, _i64,                          # q
+         _p, _p, ctypes.c_int, _i64, _i64, _i64,  # k, v caches
+         _p, _i64, _i32,                          # block tables
+         _p, _i32, _i32, _i32, _i32, _i32,        # ctx, batch, nh, nkv, hd, bs
+         _f32, _i32, _p],                         # scale, wgs, stream
     ),  # fmt: skip
     "pkv_rms_norm": (
         ctypes.c_int,

@@ -222,39 +222,16 @@ def paged_decode_attention(
     """
     del block_n
     what = "paged_decode_attention"
-    dev = _native.require_gpu(what, q, k_cache, v_cache, block_tables, context_lens)
-    if q.dim() != 3 or k_cache.dim() != 3 or v_cache.dim() != 3:
-        raise ValueError(f"{what}: q, k_cache, v_cache must be 3-D")
+    dev = _check_decode_args(what, q, k_cache, v_cache, block_tables, context_lens, block_size)
     b, nh, hd = q.shape
     nkv = k_cache.shape[1]
-    if v_cache.shape != k_cache.shape or k_cache.shape[2] != hd:
-        raise ValueError(f"{what}: cache shapes {tuple(k_cache.shape)}, "
-                         f"{tuple(v_cache.shape)} do not match q {tuple(q.shape)}")  # fmt: skip
-    if nh % nkv:
-        raise ValueError(f"{what}: {nh} query heads not a multiple of {nkv} KV heads")
-    if hd not in SUPPORTED_HEAD_DIMS:
-        raise ValueError(f"{what}: head_dim {hd} not in {SUPPORTED_HEAD_DIMS}")
-    if q.dtype != k_cache.dtype or v_cache.dtype != k_cache.dtype:
-        raise TypeError(f"{what}: q {q.dtype} and caches {k_cache.dtype}/{v_cache.dtype} "
-                        "must share one dtype")  # fmt: skip
-    if k_cache.stride() != v_cache.stride() or k_cache.stride(2) != 1:
-        raise ValueError(f"{what}: k_cache and v_cache need equal strides, unit in head_dim")
-    if block_tables.dtype != torch.int32 or context_lens.dtype != torch.int32:
-        raise TypeError(f"{what}: block_tables and context_lens must be int32")
-    if block_tables.dim() != 2 or block_tables.shape[0] != b or block_tables.stride(1) != 1:
-        raise ValueError(f"{what}: block_tables must be [B, max_blocks] with unit column stride")
-    if context_lens.shape != (b,) or not context_lens.is_contiguous():
-        raise ValueError(f"{what}: context_lens must be a contiguous [B] tensor")
-    if block_size <= 0:
-        raise ValueError(f"{what}: block_size must be positive")
     kv_code = _native.dtype_code(k_cache.dtype, what)
 
     q = q.contiguous()
     if out is None:
         out = torch.empty_like(q)
-    elif out.shape != q.shape or out.dtype not in (q.dtype, torch.float32) or \
-            out.stride(2) != 1 or out.device != dev:  # fmt: skip
-        raise ValueError(f"{what}: out must be [B, nh, hd] of {q.dtype} or float32 on {dev}")
+    else:
+        _check_out(what, out, q, dev)
     if b == 0:
         return out
 
@@ -294,6 +271,85 @@ def paged_decode_attention(
     )  # fmt: skip
     _native.check(status, what)
     return out
+
+
+def paged_decode_attention_noalloc(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    context_lens: torch.Tensor,
+    block_size: int,
+    *,
+    out: torch.Tensor,
+    num_workgroups: int | None = None,
+) -> torch.Tensor:
+    """``paged_decode_attention`` for callers that cannot allocate: the split-K scratch
+    is a static per-GPU device array of the library (C ``pkv_paged_decode_noalloc``), the
+    result goes to the caller's ``out`` ([B, nh, hd], q.dtype or float32), and q must be
+    contiguous. Same kernels and results as ``paged_decode_attention`` at the same
+    ``num_workgroups``. Shapes whose scratch exceeds ``_native.PKV_NOALLOC_SCRATCH_BYTES``
+    raise ValueError; calls that overlap on one GPU (other streams) race on the scratch.
+    No counterpart in the reference."""
+    what = "paged_decode_attention_noalloc"
+    dev = _check_decode_args(what, q, k_cache, v_cache, block_tables, context_lens, block_size)
+    b, nh, hd = q.shape
+    nkv = k_cache.shape[1]
+    if not q.is_contiguous():
+        raise ValueError(f"{what}: q must be contiguous (no copy is made)")
+    _check_out(what, out, q, dev)
+    if b == 0:
+        return out
+    if num_workgroups is None:
+        num_workgroups = decode_workgroups(dev, q.dtype, hd, nh, nkv)
+    status = _native.lib().pkv_paged_decode_noalloc(
+        out.data_ptr(), _native.dtype_code(out.dtype, what), out.stride(0), out.stride(1),
+        q.data_ptr(), q.stride(0), q.stride(1),
+        k_cache.data_ptr(), v_cache.data_ptr(), _native.dtype_code(k_cache.dtype, what),
+        k_cache.stride(0), k_cache.stride(1), k_cache.shape[0],
+        block_tables.data_ptr(), block_tables.stride(0), block_tables.shape[1],
+        context_lens.data_ptr(), b, nh, nkv, hd, block_size, hd**-0.5, num_workgroups,
+        _native.stream_of(dev),
+    )  # fmt: skip
+    _native.check(status, what)
+    return out
+
+
+def _check_out(what: str, out: torch.Tensor, q: torch.Tensor, dev: torch.device) -> None:
+    if out.shape != q.shape or out.dtype not in (q.dtype, torch.float32) or \
+            out.stride(2) != 1 or out.device != dev:  # fmt: skip
+        raise ValueError(f"{what}: out must be [B, nh, hd] of {q.dtype} or float32 on {dev}")
+
+
+def _check_decode_args(what, q, k_cache, v_cache, block_tables, context_lens,
+                       block_size) -> torch.device:  # fmt: skip
+    """The decode entry points' argument checks (before any launch); returns the device."""
+    dev = _native.require_gpu(what, q, k_cache, v_cache, block_tables, context_lens)
+    if q.dim() != 3 or k_cache.dim() != 3 or v_cache.dim() != 3:
+        raise ValueError(f"{what}: q, k_cache, v_cache must be 3-D")
+    b, nh, hd = q.shape
+    nkv = k_cache.shape[1]
+    if v_cache.shape != k_cache.shape or k_cache.shape[2] != hd:
+        raise ValueError(f"{what}: cache shapes {tuple(k_cache.shape)}, "
+                         f"{tuple(v_cache.shape)} do not match q {tuple(q.shape)}")  # fmt: skip
+    if nh % nkv:
+        raise ValueError(f"{what}: {nh} query heads not a multiple of {nkv} KV heads")
+    if hd not in SUPPORTED_HEAD_DIMS:
+        raise ValueError(f"{what}: head_dim {hd} not in {SUPPORTED_HEAD_DIMS}")
+    if q.dtype != k_cache.dtype or v_cache.dtype != k_cache.dtype:
+        raise TypeError(f"{what}: q {q.dtype} and caches {k_cache.dtype}/{v_cache.dtype} "
+                        "must share one dtype")  # fmt: skip
+    if k_cache.stride() != v_cache.stride() or k_cache.stride(2) != 1:
+        raise ValueError(f"{what}: k_cache and v_cache need equal strides, unit in head_dim")
+    if block_tables.dtype != torch.int32 or context_lens.dtype != torch.int32:
+        raise TypeError(f"{what}: block_tables and context_lens must be int32")
+    if block_tables.dim() != 2 or block_tables.shape[0] != b or block_tables.stride(1) != 1:
+        raise ValueError(f"{what}: block_tables must be [B, max_blocks] with unit column stride")
+    if context_lens.shape != (b,) or not context_lens.is_contiguous():
+        raise ValueError(f"{what}: context_lens must be a contiguous [B] tensor")
+    if block_size <= 0:
+        raise ValueError(f"{what}: block_size must be positive")
+    return dev
 
 
 def _check_prefix_groups(pg: PrefixGroups, batch: int, dev: torch.device, what: str) -> None:

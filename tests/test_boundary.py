@@ -40,8 +40,23 @@ def test_header_symbols_are_exported_and_bound():
 def test_status_strings():
     lib = _native.lib()
     assert lib.pkv_status_string(0) == b"ok"
-    for code in (-1, -2, -3, -4, -5):
+    for code in (-1, -2, -3, -4, -5, -6, -7):
         assert lib.pkv_status_string(code) != b"unknown error"
+
+
+def test_noalloc_decode_refuses_oversized_scratch_before_launch():
+    """pkv_paged_decode_noalloc checks its workspace against the static scratch
+    (PKV_NOALLOC_SCRATCH_BYTES) before touching any pointer or the GPU: a work split
+    whose records exceed it returns PKV_E_SCRATCH (the pointers here are never read)."""
+    lib = _native.lib()
+    fake = 1 << 20  # aligned, never dereferenced
+    need = lib.pkv_decode_workspace_bytes(1 << 20, 1, 64, 256)
+    assert need > _native.PKV_NOALLOC_SCRATCH_BYTES
+    st = lib.pkv_paged_decode_noalloc(fake, 2, 64 * 256, 256, fake, 64 * 256, 256, fake, fake,
+                                      2, 8 * 256, 256, 1024, fake, 64, 64, fake, 1, 64, 8,
+                                      256, 16, 0.0625, 1 << 20, None)  # fmt: skip
+    assert st == -7
+    assert b"no-alloc" in lib.pkv_status_string(st)
 
 
 def test_workspace_arithmetic():
