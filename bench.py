@@ -14,7 +14,9 @@ one hipGraph and replayed (the reference runs decode steps as CUDA-graph replays
 engine/runtime/cuda_graphs.py), between events bracketed by synchronize(). ``eager_us``
 is the mean of per-call events around eager calls (includes per-call launch costs).
 ``roofline.achieved`` = algorithmic K+V bytes (sum(ctx) * 2 * nkv * hd * 2 B) / the
-graph-replay time per layer-step. ``cpu_baseline`` times the C oracle on host cores.
+graph-replay time per layer-step. ``cpu_baseline`` times the reference's CPU path (torch
+index_copy_ append + gather -> fp32 softmax -> PV) on the host cores, for the bench's
+config and, at config 2, for config 1 beside it.
 
 ``--config c5`` measures the mixed chunked-prefill step of config 5 instead (append of
 2,168 rows, MFMA prefill of 4 x 512-token chunks, decode of 120 sequences); its line
@@ -40,6 +42,7 @@ sys.path.insert(0, os.path.join(ROOT, "inference-engine_amd"))
 HBM_PEAK_GBPS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_traffic.json")
+DECODE_SOURCES = ("common.h", "decode.hip")  # what the stream pass is compiled from
 METRIC = "paged decode attn us/layer-step + achieved HBM GB/s (% of 8 TB/s), 3B shape"
 
 
@@ -77,32 +80,76 @@ def cpu_model() -> str:
     return "unknown CPU"
 
 
-def cpu_baseline(step, budget_s: float) -> dict:
-    """The C oracle (double-accumulating scalar restatement of the reference's CPU
-    gather-then-attention path) on the full config batch, OpenMP over host cores."""
-    from oracle import oracle
+def host_threads() -> tuple[int, str]:
+    """Threads for the CPU baseline: the cores this process may run on, capped at the
+    pool's per-GPU CPU share (OMP_NUM_THREADS, 16 on the GPU boxes, which run one GPU per
+    job on a shared host); and a note of what the host reports."""
+    avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    share = int(os.environ.get("OMP_NUM_THREADS") or avail or 1)
+    n = max(1, min(avail or 1, share))
+    return n, (f"os.cpu_count()={os.cpu_count()}, affinity={avail}, "
+               f"OMP_NUM_THREADS={os.environ.get('OMP_NUM_THREADS')}")
 
-    threads = min(16, os.cpu_count() or 1)
-    args = (step.q.cpu(), step.k_cache.cpu(), step.v_cache.cpu(), step.block_tables.cpu(),
-            step.context_lens.cpu(), step.block_size)  # fmt: skip
-    oracle.decode_attention(*args, threads=threads)  # warm-up
+
+def cpu_baseline(step, budget_s: float) -> dict:
+    """The reference's CPU path for one decode layer-step (index_copy_ append, then the
+    per-sequence gather -> fp32 softmax -> PV of reference_decode_attention), restated with
+    torch CPU ops in oracle/torch_path.py, on a CPU copy of the step's inputs: median of
+    >= 5 timed reps after one warm-up, within about ``budget_s`` seconds."""
+    import torch
+
+    from oracle import torch_path
+
+    n, note = host_threads()
+    torch.set_num_threads(n)
+    cpu = {k: getattr(step, k).cpu() for k in ("q", "k_cache", "v_cache", "block_tables",
+                                                "context_lens", "new_k", "new_v", "slot_mapping")}
+
+    def run():
+        torch_path.decode_layer_step(cpu["q"], cpu["k_cache"], cpu["v_cache"],
+                                     cpu["block_tables"], cpu["context_lens"], step.block_size,
+                                     cpu["new_k"], cpu["new_v"], cpu["slot_mapping"])  # fmt: skip
+
+    run()  # warm-up
     times = []
     t_start = time.perf_counter()
-    while len(times) < 2 or (time.perf_counter() - t_start < budget_s and len(times) < 20):
+    while len(times) < 5 or (time.perf_counter() - t_start < budget_s and len(times) < 30):
         t0 = time.perf_counter()
-        oracle.decode_attention(*args, threads=threads)
+        run()
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
     return {
         "value": round(med * 1e6, 1),
         "unit": "us/layer-step",
         "gbps": round(step.kv_bytes() / med / 1e9, 2),
-        "cores": threads,
+        "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"full {step.name} layer-step (batch {step.batch}), median of {len(times)} "
-                  f"reps; C oracle in float64, OpenMP {threads} threads, host "
-                  f"os.cpu_count()={os.cpu_count()}, {cpu_model()}",
+        "sample": f"full {step.name} layer-step (batch {step.batch}): the reference's CPU "
+                  f"path (index_copy_ append + per-sequence gather, fp32 softmax, PV) in torch "
+                  f"on CPU, median of {len(times)} reps; torch threads "
+                  f"{torch.get_num_threads()} ({note}), {cpu_model()}",
     }  # fmt: skip
+
+
+def traffic_of(step_name: str) -> tuple[int | None, str]:
+    """HBM bytes per dispatch of the decode stream pass from the committed rocprofv3
+    counter summary, if it was measured on the decode sources built now (their SHA-256
+    is stored with it); otherwise None and why."""
+    import hashlib
+
+    if not os.path.exists(TRAFFIC_FILE):
+        return None, "no counter profile"
+    with open(TRAFFIC_FILE) as f:
+        entry = json.load(f).get(step_name)
+    if not entry:
+        return None, f"no counter profile for {step_name}"
+    h = hashlib.sha256()
+    for name in DECODE_SOURCES:
+        with open(os.path.join(ROOT, "inference-engine_amd", "csrc", name), "rb") as f:
+            h.update(f.read())
+    if entry.get("sources_sha256") != h.hexdigest():
+        return None, "stale: the counter profile was taken on other decode sources"
+    return entry["bytes"], f"{entry['source']} (sources {h.hexdigest()[:12]})"
 
 
 def eager_us(torch, fns, steps: int, warmup: int) -> list[float]:
@@ -198,10 +245,7 @@ def bench_decode(args, torch) -> dict:
 
     kv_bytes = step.kv_bytes()
     gbps = kv_bytes / (value * 1e-6) / 1e9
-    traffic = None
-    if os.path.exists(TRAFFIC_FILE):
-        with open(TRAFFIC_FILE) as f:
-            traffic = (json.load(f).get(step.name) or {}).get("bytes")
+    traffic, traffic_source = traffic_of(step.name)
     line = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -236,6 +280,7 @@ def bench_decode(args, torch) -> dict:
             "frac": round(gbps / HBM_PEAK_GBPS, 4),
             "traffic": traffic,
         },
+        "traffic_source": traffic_source,
         "kv_bytes_per_step": kv_bytes,
         "eager_us": round(eager_mean, 2),
         "eager_median_us": round(statistics.median(per), 2),
@@ -251,6 +296,11 @@ def bench_decode(args, torch) -> dict:
                                   line["unique_kv_bytes_per_step"]))  # fmt: skip
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(step, args.cpu_seconds)
+        if step.name.startswith("c2"):  # config 1 beside it: the reference's CPU-run case
+            from engine import workloads
+
+            line["cpu_baseline_c1"] = cpu_baseline(workloads.config1("cpu", seed=args.seed),
+                                                   min(5.0, args.cpu_seconds))  # fmt: skip
     return line
 
 
