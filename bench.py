@@ -210,10 +210,7 @@ def decode_setup(args, torch):
     pools = [(step.k_cache, step.v_cache)]
     for _ in range(args.layers - 1):
         pools.append((torch.randn_like(step.k_cache), torch.randn_like(step.v_cache)))
-    b, nh, hd = step.q.shape
-    nkv = step.k_cache.shape[1]
-    wgs = args.workgroups or pa.decode_workgroups(dev, step.q.dtype, hd, nh, nkv)
-    return step, pools, torch.empty_like(step.q), wgs
+    return step, pools, torch.empty_like(step.q), args.workgroups  # None: default split
 
 
 def bench_decode(args, torch) -> dict:
@@ -224,6 +221,10 @@ def bench_decode(args, torch) -> dict:
     b, nh, hd = step.q.shape
     nkv = step.k_cache.shape[1]
     w = step.block_tables.shape[1]
+    # What the decode call runs: 0 = the one-kernel per-sequence split pass, else the
+    # stream-K pass over that many workgroups (plus its combine).
+    plan = wgs or pa.default_workgroups(step.q.device, step.q.dtype, hd, nh, nkv, b, w,
+                                        step.block_size)  # fmt: skip
 
     def attn_fn(k, v):
         return lambda: pa.paged_decode_attention(
@@ -268,7 +269,8 @@ def bench_decode(args, torch) -> dict:
             "block_size": step.block_size,
             "table_width": w,
             "sum_ctx": int(step.context_lens.sum()),
-            "workgroups": wgs,
+            "workgroups": plan,
+            "decode_pass": "split (one kernel)" if plan == 0 else "stream-k + combine",
             "layer_pools": len(pools),
             "timing": "eager" if args.no_graph else "hipgraph replay",
         },
@@ -435,7 +437,7 @@ def bench_mixed(args, torch) -> dict:
     out_c = torch.empty_like(m.q_chunks)
     out_d = torch.empty_like(d.q)
     nh, hd = d.q.shape[1], d.q.shape[2]
-    wgs = args.workgroups or pa.decode_workgroups(dev, d.q.dtype, hd, nh, d.k_cache.shape[1])
+    wgs = args.workgroups  # None: the library's default split
 
     def append():
         kv_append(m.k_cache, m.v_cache, m.new_k, m.new_v, m.slot_mapping)

@@ -97,6 +97,16 @@ int pkv_decode_slots(int64_t* slots, const int32_t* block_tables, int64_t table_
 int32_t pkv_decode_workgroups(int kv_dtype, int32_t head_dim, int32_t num_heads,
                               int32_t num_kv_heads);
 
+/*
+ * What num_workgroups = 0 (the default split) of pkv_paged_decode runs for this shape
+ * without cascade extras: 0 for the one-kernel split pass (no workspace), else the
+ * stream-K workgroup count (pkv_decode_workgroups), whose workspace the caller passes.
+ * Depends on static shapes and the device only. Negative: a PKV_E_* code.
+ */
+int32_t pkv_decode_default_workgroups(int kv_dtype, int32_t head_dim, int32_t num_heads,
+                                      int32_t num_kv_heads, int32_t batch, int32_t max_blocks,
+                                      int32_t block_size);
+
 /* Bytes of scratch pkv_paged_decode needs for num_workgroups (0 when it is 1): one
  * 16-byte merge plan per sequence, then the partial records of sequences cut by a
  * range boundary. Any contents. */
@@ -116,9 +126,17 @@ int64_t pkv_decode_workspace_bytes(int32_t num_workgroups, int32_t batch, int32_
  * block_tables: int32 [batch, >= max_blocks] with row stride table_stride.
  * head_dim in {16, 32, 64, 128, 256}.
  * Work split: the contexts of all sequences, laid end to end, are divided evenly among
- * num_workgroups workgroups (pkv_decode_workgroups gives the default); a second kernel
- * merges the pieces of sequences cut by a boundary. num_workgroups > 1 needs a 16-byte
- * aligned scratch `workspace` of pkv_decode_workspace_bytes() bytes (any contents).
+ * num_workgroups workgroups; a second kernel merges the pieces of sequences cut by a
+ * boundary. num_workgroups > 1 needs a 16-byte aligned scratch `workspace` of
+ * pkv_decode_workspace_bytes() bytes (any contents). num_workgroups = 0 asks for the
+ * library's default, chosen from static shapes only (so a captured graph stays valid
+ * for every context length): small batches of 16-bit K/V at head_dim 64 or 128 whose
+ * (sequence, KV head) pairs fit the CUs and whose table width is at most 2,048 tokens
+ * run one kernel with one workgroup per (sequence, KV head, sub-group of its query
+ * heads -- as few heads as keep the workgroups within the CUs) that splits the
+ * sequence among its waves and merges in LDS (no workspace used); everything else the
+ * split above with pkv_decode_workgroups() workgroups, whose workspace size the caller
+ * passes.
  */
 int pkv_paged_decode(void* out, int out_dtype, int64_t out_stride_b, int64_t out_stride_h,
                      const void* q, int64_t q_stride_b, int64_t q_stride_h,

@@ -152,6 +152,7 @@ constexpr int kQuadXor1 = 0xB1;     // quad_perm [1,0,3,2]
 constexpr int kQuadXor2 = 0x4E;     // quad_perm [2,3,0,1]
 constexpr int kRowHalfMirror = 0x141;
 constexpr int kRowMirror = 0x140;
+constexpr int kRowRor8 = 0x128;  // rotate by 8 within each 16-lane row: lane c <-> c ^ 8
 
 // Sum over aligned groups of W lanes; every lane of a group gets the group's sum.
 // After the two quad steps the value is uniform inside each quad, so the half-mirror

@@ -478,7 +478,77 @@ template <int DT> __device__ __forceinline__ void unpack16v(u32x4 r, float* f) {
 }
 
 
-template <int DT, int GPW, bool FAST, int HD>
+// ---------------------------------------------------------------------------------
+// Per-sequence split pass for small batches (one launch, no combine, no workspace):
+// paged_decode_mfma_kernel with SPLIT. Workgroup (b, task) takes sequence b for one KV
+// head's query heads h0 .. h0 + GPW - 1; its kSplitWaves waves take equal 16-token-
+// aligned shares of the context (each the same matrix-core piece as a stream-K wave)
+// and merge their softmax states through LDS: with M = max_s m_s,
+// out = sum_s 2^(m_s - M) acc_s / sum_s 2^(m_s - M) l_s. Chosen by the host only from
+// static shapes (batch, KV heads, table width), so a graph captured with it serves every
+// context length: when the (sequence, task) pairs fit the CUs and the table's width
+// bounds every wave's share to kSplitMaxTiles tiles. The step is then a few dependent
+// memory trips long instead of two launches.
+// ---------------------------------------------------------------------------------
+
+constexpr int kSplitWaves = 8;
+constexpr int kSplitMaxTiles = 16;      // per wave, from the table width (static)
+constexpr int kSplitMaxColumns = 2048;  // table columns staged in LDS
+
+// The split pass's merge: every wave's state (lanes grp == 0, col < HD / 8 hold acc[g]
+// for head dims 8 col .. 8 col + 7; lh, mh are the same in every lane) goes to LDS, then
+// wave g < GPW merges query head h0 + g and stores it. All waves call it.
+template <int DT, int GPW, int HD>
+__device__ __forceinline__ void split_merge(const DecodeArgs& a, int b, int h0,
+                                            const float (&acc)[GPW][8], const float (&lh)[GPW],
+                                            const float (&mh)[GPW]) {
+  constexpr int W = kSplitWaves, VC = HD / 8;
+  constexpr int DPL = HD / kWave;  // head dims per lane in the merge (2 or 1)
+  using S = typename Elt<DT>::S;
+  __shared__ __attribute__((aligned(16))) float part_acc[W][GPW][HD];
+  __shared__ float part_ml[W][GPW][2];
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int col = lane & 15, grp = lane >> 4;
+  if (grp == 0 && col < VC) {
+#pragma unroll
+    for (int g = 0; g < GPW; ++g) {
+      float4* dst = reinterpret_cast<float4*>(&part_acc[wave][g][8 * col]);
+      dst[0] = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
+      dst[1] = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
+      if (col == 0) {
+        part_ml[wave][g][0] = mh[g];
+        part_ml[wave][g][1] = lh[g];
+      }
+    }
+  }
+  __syncthreads();
+  if (wave >= GPW) return;
+  const int g = wave;
+  float mmax = -INFINITY;
+#pragma unroll
+  for (int s = 0; s < W; ++s) mmax = fmaxf(mmax, part_ml[s][g][0]);
+  const float mref = mmax == -INFINITY ? 0.f : mmax;  // nothing live: weights 0
+  float l = 0.f, o[DPL];
+#pragma unroll
+  for (int k = 0; k < DPL; ++k) o[k] = 0.f;
+#pragma unroll
+  for (int s = 0; s < W; ++s) {
+    const float wgt = __builtin_amdgcn_exp2f(part_ml[s][g][0] - mref);  // empty share: 0
+    l = __builtin_fmaf(wgt, part_ml[s][g][1], l);
+#pragma unroll
+    for (int k = 0; k < DPL; ++k) o[k] = __builtin_fmaf(wgt, part_acc[s][g][DPL * lane + k], o[k]);
+  }
+  const float inv = l > 0.f ? 1.f / l : 0.f;  // empty context: 0
+  const int64_t e = b * a.out_sb + (int64_t)(h0 + g) * a.out_sh + DPL * lane;
+#pragma unroll
+  for (int k = 0; k < DPL; ++k) {
+    const float v = o[k] * inv;
+    if (a.out_f32) reinterpret_cast<float*>(a.out)[e + k] = v;
+    else reinterpret_cast<S*>(a.out)[e + k] = Elt<DT>::from_f32(v);
+  }
+}
+
+template <int DT, int GPW, bool FAST, int HD, bool SPLIT>
 __global__ void __launch_bounds__(512)
 paged_decode_mfma_kernel(const DecodeArgs a) {
   // hd 128: a step is one 16-token tile, four 32-dim MFMA k-blocks, V rows over all 16
@@ -493,14 +563,33 @@ paged_decode_mfma_kernel(const DecodeArgs a) {
   using MMA = Mfma16x16x32<DT>;
 
   const int lane = threadIdx.x & (kWave - 1);
-  const int task = blockIdx.y * (blockDim.x / kWave) + (threadIdx.x / kWave);
+  // Stream-K: wave = task (KV head and head sub-group), workgroup x = unit range.
+  // SPLIT: workgroup = (sequence blockIdx.x, task blockIdx.y), wave = share of it.
+  const int task = SPLIT ? (int)blockIdx.y
+                         : (int)(blockIdx.y * (blockDim.x / kWave) + (threadIdx.x / kWave));
   const int kvh = task / a.nsub;
-  if (kvh >= a.nkv) return;
+  if (!SPLIT && kvh >= a.nkv) return;
   const int h0 = kvh * a.groups + (task - kvh * a.nsub) * GPW;
   const int w = blockIdx.x;
 
   int64_t total, rs, re, ub;
-  int b = locate_range(a, w, &total, &rs, &re, &ub);
+  int b;
+  // SPLIT: the sequence's block table row is staged in LDS by the whole workgroup, in
+  // the same memory trip as each wave's context length (the split's tables hold at most
+  // kSplitMaxColumns entries), so no wave waits for its length before its block ids.
+  __shared__ int split_table[SPLIT ? kSplitMaxColumns : 1];
+  int split_n = 0;
+  if constexpr (SPLIT) {
+    total = rs = ub = 0;
+    re = 1;
+    b = blockIdx.x;
+    split_n = clamped_ctx(a, b);
+    for (int j = threadIdx.x; j < a.max_blocks; j += blockDim.x)
+      split_table[j] = a.tables[(int64_t)b * a.table_stride + j];
+    __syncthreads();
+  } else {
+    b = locate_range(a, w, &total, &rs, &re, &ub);
+  }
   if (rs >= re) return;
 
   const int col = lane & 15, grp = lane >> 4;
@@ -514,16 +603,37 @@ paged_decode_mfma_kernel(const DecodeArgs a) {
   for (int r = 0; r < 4; ++r) v_off[r] = (4 * grp + r) * a.kv_ss + 8 * (HD == 64 ? (col & 7) : col);
 
   for (int64_t u = rs; u < re && b < a.batch; ++b) {
-    const int n = clamped_ctx(a, b);
-    const int64_t ue = ub + units_of(a, n);
-    const int64_t seg_end = ue < re ? ue : re;
-    const bool whole = (u == ub) && (seg_end == ue);
-    const int slot = (u == rs) ? 0 : 1;
-    const int t0 = (int)(u - ub) * TILE;
-    const int t1 = min(n, (int)(seg_end - ub) * TILE);
-    if (u == ub && task == 0 && lane == 0) write_desc(a, b, w, ub, ue, rs, total);
-    u = seg_end;
-    ub = ue;
+    int n;
+    if constexpr (SPLIT) n = split_n;
+    else n = clamped_ctx(a, b);
+    int t0, t1, slot = 0;
+    bool whole = true;
+    if constexpr (SPLIT) {  // this wave's 16-token-aligned share of the context
+      constexpr int W = kSplitWaves;
+      // Wave-uniform (readfirstlane): the full / partial / empty tile branches below are
+      // then scalar branches, and the compiler does not wait for one step's loads before
+      // issuing the next step's.
+      const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+      const int nu = __builtin_amdgcn_readfirstlane(n);
+      const int units = (nu + TILE - 1) / TILE;
+      t0 = (wave * units / W) * TILE;
+      t1 = min(nu, ((wave + 1) * units / W) * TILE);
+      u = re;
+    } else {
+      const int64_t ue = ub + units_of(a, n);
+      const int64_t seg_end = ue < re ? ue : re;
+      whole = (u == ub) && (seg_end == ue);
+      slot = (u == rs) ? 0 : 1;
+      t0 = (int)(u - ub) * TILE;
+      t1 = min(n, (int)(seg_end - ub) * TILE);
+      if constexpr (HD == 64) {  // wave-uniform: scalar branches in the two-sub-tile loads
+        t0 = __builtin_amdgcn_readfirstlane(t0);
+        t1 = __builtin_amdgcn_readfirstlane(t1);
+      }
+      if (u == ub && task == 0 && lane == 0) write_desc(a, b, w, ub, ue, rs, total);
+      u = seg_end;
+      ub = ue;
+    }
 
     // Q^T as the B operand: column col = query head h0 + col.
     u32x4 qb[4];
@@ -539,7 +649,10 @@ paged_decode_mfma_kernel(const DecodeArgs a) {
     auto load_table = [&](int first_block) {
       cb = first_block;
       const int j = cb + lane;
-      tbl = j < a.max_blocks - fb ? a.tables[b * a.table_stride + fb + j] : 0;
+      if constexpr (SPLIT)  // first_block is null on the split path: fb == 0
+        tbl = j < a.max_blocks ? split_table[j] : 0;
+      else
+        tbl = j < a.max_blocks - fb ? a.tables[b * a.table_stride + fb + j] : 0;
     };
     auto block_of = [&](int p) { return a.bs_shift >= 0 ? (p >> a.bs_shift) : p / a.bs; };
 
@@ -610,72 +723,86 @@ paged_decode_mfma_kernel(const DecodeArgs a) {
       return ok;
     };
 
-    // hd 64: sub-tile u's K into kr[KB u ..] and V rows on lane columns 8u .. 8u + 7
-    // (other lanes keep theirs); returns bit r set when token 4*grp + r is live.
+    // hd 64: both 16-token sub-tiles of a step. Sub-tile u's K goes to kr[KB u ..]; the
+    // V rows on lane columns 8u .. 8u + 7 come from sub-tile u, one load per row for all
+    // lanes (lanes 0-7 address sub-tile 0's slots, lanes 8-15 sub-tile 1's), so no
+    // register is written by two loads. Bits 4u .. 4u + 3 of the result: token 4*grp + r
+    // of sub-tile u is live.
     const bool vlane0 = col < 8;  // hd 64: this lane's V rows come from sub-tile 0
-    auto load_sub = [&](int tb, u32x4* kr, u32x4* vr, int u) -> unsigned {
+    const int vd = 8 * (col & 7);
+    auto load_pair = [&](int tb, u32x4* kr, u32x4* vr) -> unsigned {
       const u32x4 z = {0, 0, 0, 0};
-      const bool vmine = (col >> 3) == u;
-      const int vd = 8 * (col & 7);
-      kr += KB * u;
       if (tb >= t1) {
 #pragma unroll
-        for (int i = 0; i < KB; ++i) kr[i] = z;
+        for (int i = 0; i < 2 * KB; ++i) kr[i] = z;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) vr[r] = vmine ? z : vr[r];
+        for (int r = 0; r < 4; ++r) vr[r] = z;
         return 0;
       }
-      if (block_of(min(tb + TILE, t1) - 1) - cb >= kWave) load_table(block_of(tb));
+      if (block_of(min(tb + STEP, t1) - 1) - cb >= kWave) load_table(block_of(tb));
       unsigned ok = 0;
       if constexpr (FAST) {
-        const int blk = block_of(tb);
-        const int bid = __builtin_amdgcn_readlane(tbl, blk - cb);
-        const int64_t slot0 = (int64_t)bid * a.bs + (tb - blk * a.bs);
-        const int live = (bid >= 0 && slot0 + TILE <= a.num_slots) ? min(TILE, t1 - tb) : 0;
-        const S* kt = kbase + slot0 * a.kv_ss;
-        const S* vt = vbase + slot0 * a.kv_ss;
-        if (live == TILE) {  // full sub-tile: precomputed offsets, no clamping
+        // One load form for full and partial sub-tiles (token index clamped to the last
+        // live one), so the only branches are on the wave-uniform live counts.
+        int live[2];
+        const S* vt[2];
 #pragma unroll
-          for (int m = 0; m < KB; ++m) kr[m] = load_kv16v(kt + k_off + 32 * m);
+        for (int u = 0; u < 2; ++u) {
+          const int tu = tb + TILE * u;
+          const int blk = block_of(tu);
+          const int bid = __builtin_amdgcn_readlane(tbl, blk - cb);
+          const int64_t slot0 = (int64_t)bid * a.bs + (tu - blk * a.bs);
+          live[u] = (tu < t1 && bid >= 0 && slot0 + TILE <= a.num_slots) ? min(TILE, t1 - tu) : 0;
+          // a dead sub-tile's lanes read pool row 0 (in bounds when any tile is live) and
+          // are masked out
+          vt[u] = vbase + (live[u] ? slot0 : 0) * a.kv_ss;
+          if (live[u] > 0) {
+            const S* kt = kbase + slot0 * a.kv_ss + min(col, live[u] - 1) * a.kv_ss + 8 * grp;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) vr[r] = vmine ? load_kv16v(vt + v_off[r]) : vr[r];
-          return 0xFu;
+            for (int m = 0; m < KB; ++m) kr[KB * u + m] = load_kv16v(kt + 32 * m);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) ok |= (unsigned)(4 * grp + r < live[u]) << (4 * u + r);
+          } else {
+#pragma unroll
+            for (int m = 0; m < KB; ++m) kr[KB * u + m] = z;
+          }
         }
-        if (live == 0) {
+        if (live[0] + live[1] > 0) {
+          const S* vl = vlane0 ? vt[0] : vt[1];
+          const int lv = max(vlane0 ? live[0] : live[1], 1);
 #pragma unroll
-          for (int i = 0; i < KB; ++i) kr[i] = z;
+          for (int r = 0; r < 4; ++r) vr[r] = load_kv16v(vl + min(4 * grp + r, lv - 1) * a.kv_ss + vd);
+        } else {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) vr[r] = vmine ? z : vr[r];
-          return 0;
-        }
-        const int kt_tok = min(col, live - 1);
-#pragma unroll
-        for (int m = 0; m < KB; ++m) kr[m] = load_kv16v(kt + kt_tok * a.kv_ss + 8 * grp + 32 * m);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int tok = 4 * grp + r;
-          vr[r] = vmine ? load_kv16v(vt + min(tok, live - 1) * a.kv_ss + vd) : vr[r];
-          ok |= (unsigned)(tok < live) << r;
+          for (int r = 0; r < 4; ++r) vr[r] = z;
         }
       } else {
-        const int p = tb + col;
-        const int blk = block_of(p);
-        const int bid = __shfl(tbl, blk - cb);
-        const int64_t sl = (int64_t)bid * a.bs + (p - blk * a.bs);
-        const bool kon = p < t1 && sl >= 0 && sl < a.num_slots;
-        const int64_t kslot = kon ? sl : -1;
+        int64_t kslot[2];
 #pragma unroll
-        for (int m = 0; m < KB; ++m)
-          kr[m] = kon ? load_kv16v(kbase + kslot * a.kv_ss + 8 * grp + 32 * m) : z;
+        for (int u = 0; u < 2; ++u) {
+          const int p = tb + TILE * u + col;
+          const int blk = block_of(p);
+          const int bid = __shfl(tbl, blk - cb);
+          const int64_t sl = (int64_t)bid * a.bs + (p - blk * a.bs);
+          const bool kon = p < t1 && sl >= 0 && sl < a.num_slots;
+          kslot[u] = kon ? sl : -1;
+#pragma unroll
+          for (int m = 0; m < KB; ++m)
+            kr[KB * u + m] = kon ? load_kv16v(kbase + kslot[u] * a.kv_ss + 8 * grp + 32 * m) : z;
+        }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int src = 4 * grp + r;
-          const int lo = __shfl((int)(kslot & 0xFFFFFFFF), src);
-          const int hi = __shfl((int)(kslot >> 32), src);
-          const int64_t vs = ((int64_t)hi << 32) | (uint32_t)lo;
-          const bool on = vs >= 0;
-          vr[r] = vmine ? (on ? load_kv16v(vbase + vs * a.kv_ss + vd) : z) : vr[r];
-          ok |= (unsigned)on << r;
+          const int src = 4 * grp + r;  // the K lane holding this row's token
+          int64_t vs[2];
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const int lo = __shfl((int)(kslot[u] & 0xFFFFFFFF), src);
+            const int hi = __shfl((int)(kslot[u] >> 32), src);
+            vs[u] = ((int64_t)hi << 32) | (uint32_t)lo;
+            ok |= (unsigned)(vs[u] >= 0) << (4 * u + r);
+          }
+          const int64_t v = vlane0 ? vs[0] : vs[1];
+          vr[r] = v >= 0 ? load_kv16v(vbase + v * a.kv_ss + vd) : z;
         }
       }
       return ok;
@@ -683,7 +810,7 @@ paged_decode_mfma_kernel(const DecodeArgs a) {
     // A step's loads; ok bits 4u .. 4u + 3 mark sub-tile u's live tokens.
     auto load_step = [&](int tb, u32x4* kr, u32x4* vr) -> unsigned {
       if constexpr (NS == 1) return load_tile(tb, kr, vr);
-      else return load_sub(tb, kr, vr, 0) | (load_sub(tb + TILE, kr, vr, 1) << 4);
+      else return load_pair(tb, kr, vr);
     };
 
     float m_run = -INFINITY;  // running max of head column col (same in all 4 rows)
@@ -816,7 +943,7 @@ paged_decode_mfma_kernel(const DecodeArgs a) {
 #pragma unroll
       for (int d = 0; d < 8; ++d) {
         acc[g][d] = rows_sum(acc[g][d]);
-        if constexpr (NS == 2) acc[g][d] += __shfl_xor(acc[g][d], 8);
+        if constexpr (NS == 2) acc[g][d] += dpp<kRowRor8>(acc[g][d]);  // lanes c, c ^ 8
       }
     float lh[GPW], mh[GPW];
 #pragma unroll
@@ -825,6 +952,10 @@ paged_decode_mfma_kernel(const DecodeArgs a) {
       mh[g] = row_bcast(m_run, g);
     }
 
+    if constexpr (SPLIT) {
+      split_merge<DT, GPW, HD>(a, b, h0, acc, lh, mh);
+      return;
+    }
     if (grp == 0 && col < VC) {  // lane c writes head dims 8c .. 8c + 7
       const int d0 = 8 * col;
       if (whole) {
@@ -1127,7 +1258,7 @@ template <int DT, int HD> constexpr bool use_mfma() {
 }
 template <int DT, int HD, int GPW> const void* decode_kernel() {
   if constexpr (use_mfma<DT, HD>())
-    return reinterpret_cast<const void*>(&paged_decode_mfma_kernel<DT, GPW, true, HD>);
+    return reinterpret_cast<const void*>(&paged_decode_mfma_kernel<DT, GPW, true, HD, false>);
   else
     return reinterpret_cast<const void*>(&paged_decode_stream_kernel<DT, HD, GPW>);
 }
@@ -1144,9 +1275,9 @@ struct LaunchDecode {
     const dim3 grid((unsigned)a->num_wg, (unsigned)ygrid), block(kWave * wpg);
     if constexpr (use_mfma<DT, HD>()) {
       if (a->bs % 16 == 0)
-        hipLaunchKernelGGL((paged_decode_mfma_kernel<DT, GPW, true, HD>), grid, block, 0, st, *a);
+        hipLaunchKernelGGL((paged_decode_mfma_kernel<DT, GPW, true, HD, false>), grid, block, 0, st, *a);
       else
-        hipLaunchKernelGGL((paged_decode_mfma_kernel<DT, GPW, false, HD>), grid, block, 0, st, *a);
+        hipLaunchKernelGGL((paged_decode_mfma_kernel<DT, GPW, false, HD, false>), grid, block, 0, st, *a);
     } else {
       hipLaunchKernelGGL((paged_decode_stream_kernel<DT, HD, GPW>), grid, block, 0, st, *a);
     }
@@ -1160,6 +1291,25 @@ struct LaunchDecode {
       hipLaunchKernelGGL((paged_decode_combine_kernel<DT, HD, 1>), dim3((unsigned)((pairs + 3) / 4)),
                          dim3(256), 0, st, *a);
     return hipGetLastError();
+  }
+};
+
+// The per-sequence split pass (16-bit K/V at head_dim 64 or 128 only).
+struct LaunchSplit {
+  const DecodeArgs* a;
+  int ytasks;
+  hipStream_t st;
+  template <int DT, int HD, int GPW> hipError_t run() const {
+    if constexpr (use_mfma<DT, HD>()) {
+      const dim3 grid((unsigned)a->batch, (unsigned)ytasks), block(kWave * kSplitWaves);
+      if (a->bs % 16 == 0)
+        hipLaunchKernelGGL((paged_decode_mfma_kernel<DT, GPW, true, HD, true>), grid, block, 0, st, *a);
+      else
+        hipLaunchKernelGGL((paged_decode_mfma_kernel<DT, GPW, false, HD, true>), grid, block, 0, st, *a);
+      return hipGetLastError();
+    } else {
+      return hipErrorInvalidValue;  // never chosen for these shapes
+    }
   }
 };
 
@@ -1227,6 +1377,52 @@ constexpr int kMaxDevices = 64;
 void* g_scratch_ptr[kMaxDevices] = {};
 std::mutex g_scratch_mu;
 
+// CU count of the current device, queried once per device.
+int g_cus[kMaxDevices] = {};
+std::mutex g_cus_mu;
+int device_cus(int* cus) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return PKV_E_HIP;
+  std::lock_guard<std::mutex> lock(g_cus_mu);
+  if (!g_cus[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n < 1)
+      return PKV_E_HIP;
+    g_cus[dev] = n;
+  }
+  *cus = g_cus[dev];
+  return 0;
+}
+
+// Whether a default-split call (num_workgroups == 0) takes the per-sequence split pass,
+// and with how many query heads per wave (*gpw, 0 = no): 16-bit K/V at head_dim 64 or
+// 128, no cascade extras, the table width bounds every wave's share to kSplitMaxTiles
+// tiles, and the (sequence, KV head, head sub-group) workgroups fit the CUs. The split
+// pass is bound by each wave's VALU work (its P.V runs per query head), so the fewest
+// heads per wave whose workgroups still fit the CUs is taken: more CUs at work, each
+// wave's K/V re-read by the head sub-groups from cache. Static shapes only, so a
+// captured graph stays valid for every context length.
+int choose_split(int kv_dtype, int head_dim, int batch, int num_heads, int num_kv_heads,
+                 int max_columns, int64_t max_tokens, bool extras, int* gpw) {
+  *gpw = 0;
+  const bool mfma = kv_dtype != PKV_F32 && (head_dim == 64 || head_dim == 128) &&
+                    PKV_DECODE_USE_MFMA;
+  if (!mfma || extras) return 0;
+  const int64_t tiles = (max_tokens + 15) / 16;
+  if (tiles > (int64_t)kSplitWaves * kSplitMaxTiles || max_columns > kSplitMaxColumns) return 0;
+  int cus = 0;
+  const int st = device_cus(&cus);
+  if (st) return st;
+  const int groups = num_heads / num_kv_heads;
+  for (int g = 1; g <= 4; ++g)
+    if (groups % g == 0 && (int64_t)batch * num_kv_heads * (groups / g) <= cus) {
+      *gpw = g;
+      break;
+    }
+  return 0;
+}
+
 // The current device's address of `scratch`, resolved on the first call per device (with
 // that device current) and cached. Returns 0 or a PKV_E_* / hipError_t status.
 int scratch_address(void** out) {
@@ -1261,6 +1457,19 @@ int32_t pkv_decode_workgroups(int kv_dtype, int32_t head_dim, int32_t num_heads,
   if (e != hipSuccess) return PKV_E_HIP;
   const int g = cus * (per_cu < 1 ? 1 : per_cu) / p.ygrid;
   return g < 1 ? 1 : g;
+}
+
+int32_t pkv_decode_default_workgroups(int kv_dtype, int32_t head_dim, int32_t num_heads,
+                                      int32_t num_kv_heads, int32_t batch, int32_t max_blocks,
+                                      int32_t block_size) {
+  const int bad = check_decode_shape(kv_dtype, head_dim, num_heads, num_kv_heads);
+  if (bad) return bad;
+  if (batch < 0 || max_blocks < 0 || block_size <= 0) return PKV_E_SHAPE;
+  int split_gpw = 0;
+  const int st = choose_split(kv_dtype, head_dim, batch, num_heads, num_kv_heads, max_blocks,
+                              (int64_t)max_blocks * block_size, false, &split_gpw);
+  if (st) return st;
+  return split_gpw ? 0 : pkv_decode_workgroups(kv_dtype, head_dim, num_heads, num_kv_heads);
 }
 
 int64_t pkv_decode_workspace_bytes(int32_t num_workgroups, int32_t batch, int32_t num_heads,
@@ -1309,7 +1518,7 @@ int pkv_paged_decode_ex(void* out, int out_dtype, int64_t out_stride_b, int64_t 
   if (cascade && (!prefix_out || !prefix_lse)) return PKV_E_NULL;
   if (cascade && !aligned16(prefix_out)) return PKV_E_ALIGN;
   if (!(out_dtype == kv_dtype || out_dtype == PKV_F32)) return PKV_E_DTYPE;
-  if (batch < 0 || block_size <= 0 || max_blocks < 0 || num_workgroups < 1 ||
+  if (batch < 0 || block_size <= 0 || max_blocks < 0 || num_workgroups < 0 ||
       num_workgroups > (1 << 24) || batch > (1 << 24))
     return PKV_E_SHAPE;
   if ((int64_t)max_blocks * block_size > (int64_t)1 << 30) return PKV_E_SHAPE;
@@ -1321,7 +1530,23 @@ int pkv_paged_decode_ex(void* out, int out_dtype, int64_t out_stride_b, int64_t 
       q_stride_b % vec || q_stride_h % vec || kv_stride_slot % vec || kv_stride_head % vec ||
       out_stride_b % vec || out_stride_h % vec)
     return PKV_E_ALIGN;
-  const DecodePlan p = plan_decode(num_heads, num_kv_heads);
+  DecodePlan p = plan_decode(num_heads, num_kv_heads);
+  bool split = false;
+  if (num_workgroups == 0) {  // the library's default split of the work
+    int split_gpw = 0;
+    const int st = choose_split(kv_dtype, head_dim, batch, num_heads, num_kv_heads, max_blocks,
+                                (int64_t)max_blocks * block_size,
+                                cascade || first_block || lse, &split_gpw);
+    if (st) return st;
+    split = split_gpw > 0;
+    if (split) {
+      p.gpw = split_gpw;
+      p.nsub = num_heads / num_kv_heads / split_gpw;
+    } else {
+      num_workgroups = pkv_decode_workgroups(kv_dtype, head_dim, num_heads, num_kv_heads);
+      if (num_workgroups < 1) return num_workgroups < 0 ? num_workgroups : PKV_E_HIP;
+    }
+  }
 
   DecodeArgs a;
   a.out = out;
@@ -1366,6 +1591,12 @@ int pkv_paged_decode_ex(void* out, int out_dtype, int64_t out_stride_b, int64_t 
   a.desc = nullptr;
   a.ws_acc = nullptr;
   a.ws_ml = nullptr;
+  hipStream_t st = (hipStream_t)stream;
+  if (split) {
+    a.num_wg = 1;
+    return (int)by_dtype(kv_dtype, head_dim, p.gpw,
+                         LaunchSplit{&a, num_kv_heads * p.nsub, st});
+  }
   const DecodeWs ws = decode_ws(num_workgroups, batch, num_heads, head_dim, cascade);
   if (ws.total) {
     if (!workspace || workspace_bytes < ws.total || !aligned16(workspace)) return PKV_E_WORKSPACE;
@@ -1389,7 +1620,6 @@ int pkv_paged_decode_ex(void* out, int out_dtype, int64_t out_stride_b, int64_t 
     }
   }
 
-  hipStream_t st = (hipStream_t)stream;
   return (int)by_dtype(kv_dtype, head_dim, p.gpw, LaunchDecode{&a, p.wpg, p.ygrid, st});
 }
 
@@ -1404,12 +1634,18 @@ int pkv_paged_decode_noalloc(void* out, int out_dtype, int64_t out_stride_b,
                              float scale, int32_t num_workgroups, void* stream) {
   const int bad = check_decode_shape(kv_dtype, head_dim, num_heads, num_kv_heads);
   if (bad) return bad;
-  if (batch < 0 || num_workgroups < 1 || num_workgroups > (1 << 24) || batch > (1 << 24))
+  if (batch < 0 || num_workgroups < 0 || num_workgroups > (1 << 24) || batch > (1 << 24))
     return PKV_E_SHAPE;
   // The same workspace layout the allocating entry point asks its caller for; it must
   // fit the static array (no contents need clearing: every record is written before
-  // the combine reads it, within the call).
-  const int64_t need = decode_ws(num_workgroups, batch, num_heads, head_dim, false).total;
+  // the combine reads it, within the call). The default split (0) is sized for its
+  // stream-K count, an upper bound of what it uses.
+  int sized = num_workgroups;
+  if (sized == 0 && batch > 0) {
+    sized = pkv_decode_workgroups(kv_dtype, head_dim, num_heads, num_kv_heads);
+    if (sized < 1) return sized < 0 ? sized : PKV_E_HIP;
+  }
+  const int64_t need = decode_ws(sized, batch, num_heads, head_dim, false).total;
   if (need > PKV_NOALLOC_SCRATCH_BYTES) return PKV_E_SCRATCH;
   void* ws = nullptr;
   if (need > 0 && batch > 0) {

@@ -37,6 +37,7 @@ SIGNATURES: dict[str, tuple] = {
     "pkv_copy_blocks": (ctypes.c_int, [_p, _p, _i64, _i32, _i64, _i64, _p, _i64, _p]),
     "pkv_decode_slots": (ctypes.c_int, [_p, _p, _i64, _i32, _p, _i32, _i32, _i64, _p]),
     "pkv_decode_workgroups": (_i32, [ctypes.c_int, _i32, _i32, _i32]),
+    "pkv_decode_default_workgroups": (_i32, [ctypes.c_int, _i32, _i32, _i32, _i32, _i32, _i32]),
     "pkv_decode_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32]),
     "pkv_cascade_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32]),
     "pkv_paged_decode": (

@@ -35,6 +35,7 @@ HAS_TRITON = False
 
 SUPPORTED_HEAD_DIMS = (16, 32, 64, 128, 256)
 _default_wgs: dict[tuple, int] = {}
+_default_plan: dict[tuple, int] = {}
 
 
 def available(device: torch.device) -> bool:
@@ -74,6 +75,25 @@ def decode_workgroups(device: torch.device, dtype: torch.dtype, head_dim: int,
                 num_kv_heads)  # fmt: skip
         _native.check(min(wgs, 0), "decode_workgroups")
         _default_wgs[key] = wgs
+    return wgs
+
+
+def default_workgroups(device: torch.device, dtype: torch.dtype, head_dim: int,
+                       num_heads: int, num_kv_heads: int, batch: int, max_blocks: int,
+                       block_size: int) -> int:  # fmt: skip
+    """What a call with the default split runs: 0 for the one-kernel per-sequence split
+    (small batches of 16-bit K/V at head_dim 64/128; no workspace), else the stream-K
+    workgroup count. Static shapes only (a graph captured with it stays valid)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    key = (idx, dtype, head_dim, num_heads, num_kv_heads, batch, max_blocks, block_size)
+    wgs = _default_plan.get(key)
+    if wgs is None:
+        with torch.cuda.device(idx):
+            wgs = _native.lib().pkv_decode_default_workgroups(
+                _native.dtype_code(dtype, "default_workgroups"), head_dim, num_heads,
+                num_kv_heads, batch, max_blocks, block_size)  # fmt: skip
+        _native.check(min(wgs, 0), "default_workgroups")
+        _default_plan[key] = wgs
     return wgs
 
 
@@ -210,9 +230,12 @@ def paged_decode_attention(
     Reference: engine/kernels/paged_attention.py:140-179. ``block_n`` (the reference's
     Triton tile) is accepted and ignored. Extensions: ``out`` receives the result in
     place ([B, nh, hd], q.dtype or float32 for the unrounded fp32 result) and
-    ``num_workgroups`` overrides how many workgroups share the contexts (default: as many
-    as the GPU holds at once); ``workspace`` (uint8, from ``decode_workspace``) replaces
-    the scratch otherwise taken from torch's caching allocator on each call.
+    ``num_workgroups`` sets how many workgroups share the contexts in the stream-K split
+    (default: the library's choice from static shapes -- for small batches at head_dim
+    64/128 one kernel that splits each sequence among one workgroup's waves, else as
+    many stream-K workgroups as the GPU holds at once); ``workspace`` (uint8, from
+    ``decode_workspace`` with ``decode_workgroups()``) replaces the scratch otherwise
+    taken from torch's caching allocator on each call.
     ``prefix_groups`` (from ``find_prefix_groups``) turns on cascade decode for 16-bit
     caches at head_dim 32-256: each group's shared prefix is read once for all its
     members on the matrix cores (the chunked-prefill kernel, non-causal, one fp32 part
@@ -236,15 +259,19 @@ def paged_decode_attention(
         return out
 
     max_blocks = block_tables.shape[1]
-    if num_workgroups is None:
-        num_workgroups = decode_workgroups(dev, q.dtype, hd, nh, nkv)
     lib = _native.lib()
     cascade = prefix_groups is not None and q.dtype in (torch.bfloat16, torch.float16) \
         and hd in PREFILL_HEAD_DIMS  # fmt: skip
     if cascade:
         _check_prefix_groups(prefix_groups, b, dev, what)
+    # None: the library's default (C: 0): the one-kernel split for small batches (no
+    # workspace), else the stream-K split over decode_workgroups() workgroups.
+    wg_arg = 0 if num_workgroups is None else num_workgroups
+    if num_workgroups is None:
+        num_workgroups = decode_workgroups(dev, q.dtype, hd, nh, nkv) if cascade else \
+            default_workgroups(dev, q.dtype, hd, nh, nkv, b, max_blocks, block_size)  # fmt: skip
     query = lib.pkv_cascade_workspace_bytes if cascade else lib.pkv_decode_workspace_bytes
-    ws_bytes = query(num_workgroups, b, nh, hd)
+    ws_bytes = query(num_workgroups, b, nh, hd) if num_workgroups else 0
     ws = None
     if ws_bytes and workspace is not None:
         if workspace.device != dev or workspace.dtype != torch.uint8 or \
@@ -262,7 +289,7 @@ def paged_decode_attention(
         k_cache.stride(0), k_cache.stride(1), k_cache.shape[0],
         block_tables.data_ptr(), block_tables.stride(0), max_blocks,
         context_lens.data_ptr(), b, nh, nkv, hd, block_size,
-        hd**-0.5, num_workgroups, ws.data_ptr() if ws is not None else None, ws_bytes,
+        hd**-0.5, wg_arg, ws.data_ptr() if ws is not None else None, ws_bytes,
         prefix_groups.first_block.data_ptr() if cascade else None, None,
         pre[0].data_ptr() if cascade else None, pre[1].data_ptr() if cascade else None,
         prefix_groups.prefix_row.data_ptr() if cascade else None,
@@ -301,7 +328,7 @@ def paged_decode_attention_noalloc(
     if b == 0:
         return out
     if num_workgroups is None:
-        num_workgroups = decode_workgroups(dev, q.dtype, hd, nh, nkv)
+        num_workgroups = 0  # the library's default split
     status = _native.lib().pkv_paged_decode_noalloc(
         out.data_ptr(), _native.dtype_code(out.dtype, what), out.stride(0), out.stride(1),
         q.data_ptr(), q.stride(0), q.stride(1),

@@ -75,6 +75,11 @@ def test_workspace_arithmetic():
         assert lib.pkv_decode_workgroups(2, 128, 24, 8) == -6
     assert lib.pkv_decode_workgroups(2, 96, 24, 8) == -2
     assert lib.pkv_decode_workgroups(9, 128, 24, 8) == -1
+    # the default split's plan: shape errors before any device query
+    assert lib.pkv_decode_default_workgroups(2, 96, 24, 8, 8, 32, 16) == -2
+    assert lib.pkv_decode_default_workgroups(2, 128, 24, 8, 8, 32, 0) == -2
+    if not torch.cuda.is_available():  # the plan needs the CU count
+        assert lib.pkv_decode_default_workgroups(2, 128, 24, 8, 8, 32, 16) == -6
 
 
 def _decode_args(**over):
@@ -89,7 +94,7 @@ def _decode_args(**over):
 @pytest.mark.parametrize(
     ("over", "code"),
     [({"kv_dtype": 7}, -1), ({"out_dtype": 1}, -1), ({"hd": 96}, -2), ({"nh": 20}, -2),
-     ({"wgs": 0}, -2), ({"bs": 0}, -2), ({"q": (1 << 12) + 2}, -3),
+     ({"wgs": -1}, -2), ({"bs": 0}, -2), ({"q": (1 << 12) + 2}, -3),
      ({"kss": 1020}, -3), ({"q": None}, -5),
      ({"wgs": 4}, -4)],
 )  # fmt: skip

@@ -70,7 +70,10 @@ def test_config_decode_full(name):
     _say("config", name)
     step = workloads.CONFIGS[name](DEV, seed=0)
     kc, vc = _append_both(step.k_cache, step.v_cache, step.new_k, step.new_v, step.slot_mapping)
-    _decode_both(step, kc, vc)
+    _decode_both(step, kc, vc)  # default split: config 1 takes the one-kernel split pass
+    b, nh, hd = step.q.shape
+    nkv = step.k_cache.shape[1]
+    _decode_both(step, kc, vc, num_workgroups=pa.decode_workgroups(DEV, step.q.dtype, hd, nh, nkv))
 
 
 @pytest.mark.parametrize("cascade", [False, True])

@@ -251,10 +251,13 @@ def test_decode_table_row_stride_and_graph_padding_rows():
     _check_attention(step, what="padded")
 
 
-def test_graph_capture_replay():
+@pytest.mark.parametrize("split", ["stream", "default"])
+def test_graph_capture_replay(split):
     """Append + decode captured once in a hipGraph, replayed with new lengths and tables
-    (the DecodeGraphs pattern, reference engine/runtime/cuda_graphs.py:64-108)."""
-    _say("graph capture")
+    (the DecodeGraphs pattern, reference engine/runtime/cuda_graphs.py:64-108): the
+    stream-K split with a workspace allocated outside the capture, and the default split
+    (here the one-kernel split pass, chosen from static shapes only)."""
+    _say("graph capture", split)
     b, nh, nkv, hd, bs, width, nblk = 16, 24, 8, 128, 16, 64, 1200
     k_pool = torch.randn(nblk * bs, nkv, hd, device=DEV).to(torch.bfloat16)
     v_pool = torch.randn_like(k_pool)
@@ -265,8 +268,12 @@ def test_graph_capture_replay():
     nk_s = torch.zeros(b, nkv, hd, device=DEV, dtype=torch.bfloat16)
     nv_s = torch.zeros_like(nk_s)
     out_s = torch.empty(b, nh, hd, device=DEV, dtype=torch.bfloat16)
-    wgs = pa.decode_workgroups(DEV, torch.bfloat16, hd, nh, nkv)
-    ws = pa.decode_workspace(DEV, b, nh, hd, wgs)  # allocated outside the capture
+    wgs, ws = None, None
+    if split == "stream":
+        wgs = pa.decode_workgroups(DEV, torch.bfloat16, hd, nh, nkv)
+        ws = pa.decode_workspace(DEV, b, nh, hd, wgs)  # allocated outside the capture
+    else:
+        assert pa.default_workgroups(DEV, torch.bfloat16, hd, nh, nkv, b, width, bs) == 0
 
     def body():
         kv_append(k_pool, v_pool, nk_s, nv_s, slots_s)
@@ -297,10 +304,53 @@ def test_graph_capture_replay():
         torch.cuda.synchronize()
         got = out_s.clone()
         # eager on the same (already appended) pool
-        want = pa.paged_decode_attention(q_s, k_pool, v_pool, tables_s, ctx_s, bs)
+        want = pa.paged_decode_attention(q_s, k_pool, v_pool, tables_s, ctx_s, bs,
+                                         num_workgroups=wgs)  # fmt: skip
         torch.cuda.synchronize()
         assert torch.equal(_bits(got), _bits(want)), f"replay {rep}"
+        ref = oracle.decode_attention(q_s.cpu(), k_pool.cpu(), v_pool.cpu(), tables_s.cpu(),
+                                      ctx_s.cpu(), bs, threads=THREADS)  # fmt: skip
+        assert (got.float().cpu() - ref).abs().max().item() <= ATOL + 2.0**-8 * ref.abs().max().item()
         assert torch.equal(_bits(k_pool[slots_s]), _bits(nk_s))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize(("nh", "nkv", "hd"),
+                         [(32, 8, 64), (24, 8, 128), (8, 2, 64), (16, 1, 128), (40, 8, 128)])
+@pytest.mark.parametrize("block_size", [16, 4, 12, 32])
+def test_decode_split_pass(dtype, nh, nkv, hd, block_size):
+    """The one-kernel split pass of small batches (default split, chosen from static
+    shapes: pairs fit the CUs, tables of at most 2,048 tokens): empty, one-token,
+    tile-boundary and long contexts, groups of 1-5 heads per wave (sub-groups at 5),
+    block sizes that split tiles (4, 12) or not; oracle parity and agreement with the
+    stream-K split on the same inputs."""
+    _say("decode split", dtype, nh, nkv, hd, block_size)
+    ctx = [0, 1, 17, 129, 700, 2000]
+    step = workloads.custom(ctx, nh, nkv, hd, block_size, dtype, DEV, seed=hd + block_size)
+    w = step.block_tables.shape[1]
+    assert w * block_size <= 2048
+    assert pa.default_workgroups(DEV, dtype, hd, nh, nkv, len(ctx), w, block_size) == 0
+    out32, _ = _check_attention(step, what="split")
+    assert not out32[0].any()  # empty context: 0
+    stream = torch.empty_like(out32)
+    pa.paged_decode_attention(step.q, step.k_cache, step.v_cache, step.block_tables,
+                              step.context_lens, block_size, out=stream,
+                              num_workgroups=pa.decode_workgroups(DEV, dtype, hd, nh, nkv))  # fmt: skip
+    torch.cuda.synchronize()
+    assert (out32 - stream).abs().max().item() <= 1e-5
+
+
+def test_decode_default_split_keeps_stream_k_for_large_shapes():
+    """Tables wider than 2,048 tokens, or more (sequence, task) pairs than CUs, or fp32,
+    or head_dim 256: the default split is the stream-K pass."""
+    cus = torch.cuda.get_device_properties(DEV).multi_processor_count
+    bf = torch.bfloat16
+    assert pa.default_workgroups(DEV, bf, 128, 24, 8, 64, 256, 16) > 0  # config 2
+    assert pa.default_workgroups(DEV, bf, 128, 24, 8, 8, 129, 16) > 0  # 2,064 tokens
+    assert pa.default_workgroups(DEV, bf, 128, 24, 8, cus // 8 + 1, 32, 16) > 0
+    assert pa.default_workgroups(DEV, torch.float32, 128, 24, 8, 8, 32, 16) > 0
+    assert pa.default_workgroups(DEV, bf, 256, 24, 8, 8, 32, 16) > 0
+    assert pa.default_workgroups(DEV, torch.float16, 64, 32, 8, 8, 32, 16) == 0  # config 1
 
 
 @pytest.mark.parametrize("wgs", [7, 300])
