@@ -46,6 +46,9 @@ constexpr int kWave = 64;
 #ifndef PKV_PREFILL_SETPRIO
 #define PKV_PREFILL_SETPRIO 0
 #endif
+#ifndef PKV_PREFILL_SWZ
+#define PKV_PREFILL_SWZ 1
+#endif
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 

@@ -626,10 +626,11 @@ paged_decode_mfma_kernel(const DecodeArgs a) {
       slot = (u == rs) ? 0 : 1;
       t0 = (int)(u - ub) * TILE;
       t1 = min(n, (int)(seg_end - ub) * TILE);
-      if constexpr (HD == 64) {  // wave-uniform: scalar branches in the two-sub-tile loads
-        t0 = __builtin_amdgcn_readfirstlane(t0);
-        t1 = __builtin_amdgcn_readfirstlane(t1);
-      }
+      // Wave-uniform (readfirstlane): the full / partial / empty tile branches of the
+      // loads are then scalar branches, so the compiler does not wait for one tile's
+      // loads before issuing the next tile's.
+      t0 = __builtin_amdgcn_readfirstlane(t0);
+      t1 = __builtin_amdgcn_readfirstlane(t1);
       if (u == ub && task == 0 && lane == 0) write_desc(a, b, w, ub, ue, rs, total);
       u = seg_end;
       ub = ue;

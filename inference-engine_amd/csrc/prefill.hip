@@ -176,14 +176,19 @@ template <int HD> struct PrefillShape {
   static_assert(2 * NLD < 64, "vmcnt range");
   static_assert(KT <= kWave, "a tile's block ids must fit one 64-entry table window");
   // LDS position of chunk c of key t's row is c ^ swz(t). Rows are 256 bytes (head dim
-  // 128, 16 chunks), so a chunk's bank group is its position mod 8 (a 128-byte access
-  // window). The K operand reads (ds_read_b128: 8 lanes = 8 consecutive keys, one chunk,
-  // per access) are conflict-free when swz's low 3 bits are a bijection of the key's low
-  // 3 bits; the V^T transpose reads (4 consecutive keys x chunks 2d, 2d + 1 per 16
-  // lanes) when swz's bits 1-2 are a bijection of the key's bits 0-1. swz(t) = (t2, t0,
-  // t1, t3) -- bits 0..3 -- satisfies both.
+  // 128, 16 chunks). With 64 banks (a 256-byte window), a ds_read_b128 serves 16 lanes
+  // and a ds_read_b64 32 lanes per pass: the K operand reads (16 consecutive keys, one
+  // chunk) are conflict-free when swz is a bijection of the key's low 4 bits, the V^T
+  // transpose reads (8 consecutive keys x chunks 2d, 2d + 1 per 32 lanes) when swz's
+  // bits 1-3 are a bijection of the key's bits 0-2. swz(t) = (t3, t0, t1, t2) -- bits
+  // 0..3 -- satisfies both (PKV_PREFILL_SWZ 1; measured at config 5: half the bank-
+  // conflict cycles of the 32-bank layout (t2, t0, t1, t3), same results, same time).
   __device__ static int swz(int t) {
+#if PKV_PREFILL_SWZ == 1
+    if constexpr (CH == 16) return ((t & 7) << 1) | ((t >> 3) & 1);
+#else
     if constexpr (CH == 16) return ((t << 1) & 6) | ((t >> 2) & 1) | (t & 8);
+#endif
     else return t % CH;
   }
 };

@@ -148,6 +148,63 @@ def stream_of(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
+# Opt-in checks of step metadata. The kernels never fault on bad metadata: the append
+# skips slots outside the pool, and decode / prefill leave tokens whose slot falls
+# outside the pool out of the softmax. The reference raises instead (index_copy_ and
+# its gather index the pool, engine/runtime/paged_cache.py:42-49). With the checks on
+# (environment PKV_DEBUG_CHECKS=1, or set_debug_checks(True)) every call first checks
+# its metadata on the device and raises IndexError, as the reference would. Each check
+# reads one flag back (a stream synchronisation), and is skipped while a graph is
+# being captured.
+_debug_checks = os.environ.get("PKV_DEBUG_CHECKS", "0") not in ("", "0")
+
+
+def set_debug_checks(on: bool) -> bool:
+    """Turn the metadata checks on or off; returns the previous setting."""
+    global _debug_checks
+    prev, _debug_checks = _debug_checks, bool(on)
+    return prev
+
+
+def debug_checks() -> bool:
+    """Whether this call checks its metadata: on, and no graph capture under way."""
+    if not _debug_checks:
+        return False
+    return not (torch.cuda.is_available() and torch.cuda.is_current_stream_capturing())
+
+
+def check_slots(what: str, slots: torch.Tensor, num_slots: int) -> None:
+    """IndexError unless every slot lies in [0, num_slots) (index_copy_'s rule)."""
+    if slots.numel() and bool(((slots < 0) | (slots >= num_slots)).any()):
+        bad = slots[(slots < 0) | (slots >= num_slots)][:4].tolist()
+        raise IndexError(f"{what}: slots {bad} outside the pool of {num_slots} slots")
+
+
+def check_tables(what: str, block_tables: torch.Tensor, context_lens: torch.Tensor,
+                 block_size: int, num_slots: int, first: int = 0) -> None:  # fmt: skip
+    """IndexError unless each row's first context_lens[b] tokens, read through columns
+    first.. of its table, all have a slot in [0, num_slots): the context fits the table,
+    and every used block id is non-negative with its used tokens inside the pool."""
+    w = block_tables.shape[1] - first
+    if context_lens.numel() == 0:
+        return
+    n = context_lens.long()
+    if bool(((n < 0) | (n > w * block_size)).any()):
+        raise IndexError(f"{what}: context_lens {n.min().item()}..{n.max().item()} outside "
+                         f"[0, {w * block_size}] (the table's {w} columns)")  # fmt: skip
+    if w <= 0:
+        return
+    cols = torch.arange(w, device=n.device) * block_size
+    used = (n[:, None] - cols[None]).clamp(0, block_size)  # tokens each column holds
+    bid = block_tables[:, first:].long()
+    bad = (used > 0) & ((bid < 0) | (bid * block_size + used > num_slots))
+    if bool(bad.any()):
+        row, col = (int(x) for x in bad.nonzero()[0])
+        raise IndexError(f"{what}: sequence {row} column {col + first}: block id "
+                         f"{int(bid[row, col])} outside the pool of {num_slots} slots "
+                         f"(block_size {block_size})")  # fmt: skip
+
+
 def require_gpu(what: str, *tensors: torch.Tensor) -> torch.device:
     dev = tensors[0].device
     if dev.type != "cuda":

@@ -376,6 +376,8 @@ def _check_decode_args(what, q, k_cache, v_cache, block_tables, context_lens,
         raise ValueError(f"{what}: context_lens must be a contiguous [B] tensor")
     if block_size <= 0:
         raise ValueError(f"{what}: block_size must be positive")
+    if _native.debug_checks():
+        _native.check_tables(what, block_tables, context_lens, block_size, k_cache.shape[0])
     return dev
 
 
@@ -515,6 +517,9 @@ def paged_prefill_attention(
         raise ValueError(f"{what}: block_size must be positive")
     if n_chunks == 0 or t == 0:
         return out
+    if _native.debug_checks():
+        _check_chunks(what, block_tables, context_lens, block_size, k_cache.shape[0],
+                      cu_seqlens_q, t, max_query_len)  # fmt: skip
     context_lens = context_lens.contiguous()
     cu_seqlens_q = cu_seqlens_q.contiguous()
     status = _native.lib().pkv_paged_prefill(
@@ -528,3 +533,19 @@ def paged_prefill_attention(
     )  # fmt: skip
     _native.check(status, what)
     return out
+
+
+def _check_chunks(what, block_tables, context_lens, block_size, num_slots, cu_seqlens_q,
+                  num_rows, max_query_len) -> None:  # fmt: skip
+    """Prefill metadata under the debug checks: cu_seqlens_q non-decreasing from 0 within
+    q's rows, every chunk at most max_query_len rows and no longer than its context, and
+    every context token's slot inside the pool. The kernel clamps or masks each of these
+    instead (a chunk past max_query_len loses its last rows)."""
+    cu = cu_seqlens_q.long()
+    q_len = cu[1:] - cu[:-1]
+    if int(cu[0]) != 0 or bool((q_len < 0).any()) or int(cu[-1]) > num_rows:
+        raise IndexError(f"{what}: cu_seqlens_q must rise from 0 to at most {num_rows}")
+    if bool((q_len > max_query_len).any()) or bool((q_len > context_lens.long()).any()):
+        raise IndexError(f"{what}: a chunk is longer than max_query_len {max_query_len} or "
+                         "than its context")  # fmt: skip
+    _native.check_tables(what, block_tables, context_lens, block_size, num_slots)

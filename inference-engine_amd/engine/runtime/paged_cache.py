@@ -52,7 +52,8 @@ class PagedKVCache:
 
         Same result as ``self.k[layer].index_copy_(0, slots, k.to(self.k.dtype))`` and
         the V twin (reference :42-45), in one HIP launch for both pools. Slots outside
-        the pool are skipped rather than faulting the GPU.
+        the pool are skipped rather than faulting the GPU (IndexError, as index_copy_
+        raises, with ``_native.set_debug_checks(True)`` or PKV_DEBUG_CHECKS=1).
         """
         kv_append(self.k[layer], self.v[layer], k, v, slots)
 
@@ -95,6 +96,8 @@ def kv_append(
         raise ValueError(f"{what}: pool needs unit stride in head_dim")
     if n == 0:
         return
+    if _native.debug_checks():
+        _native.check_slots(what, slots, k_pool.shape[0])
     if k.stride(2) != 1:
         k = k.contiguous()
     if v.stride(2) != 1:
@@ -136,6 +139,8 @@ def copy_blocks(
     if slots % block_size:
         raise ValueError(f"{what}: {slots} slots not a multiple of block_size {block_size}")
     elt = k_pool.element_size()
+    if _native.debug_checks():
+        _native.check_slots(what, block_mapping.reshape(-1), slots // block_size)
     block_mapping = block_mapping.contiguous()
     status = _native.lib().pkv_copy_blocks(
         k_pool.data_ptr(), v_pool.data_ptr(), k_pool.stride(0) * elt, layers,

@@ -199,3 +199,50 @@ def test_workload_generators_follow_engine_layout():
     assert len(set(src)) == 1 and len(set(dst)) == 4
     assert [r[shared - 1] for r in rows[:4]] == list(dst)
     assert c3.unique_kv_bytes() < c3.kv_bytes()
+
+
+def test_debug_checks_follow_the_kernels_masking_rule():
+    """The opt-in metadata checks (CPU tensors here: they are plain torch ops) accept
+    exactly what the kernels read in bounds: a slot is live when it is in [0, num_slots),
+    and a table column is read for the tokens the context puts in it -- a partly used
+    last block may end past a whole-block boundary as long as its used tokens fit."""
+    slots = torch.tensor([0, 5, 63])
+    _native.check_slots("t", slots, 64)
+    for bad in ([64], [-1], [3, 70]):
+        with pytest.raises(IndexError, match="outside the pool"):
+            _native.check_slots("t", torch.tensor(bad), 64)
+    _native.check_slots("t", torch.tensor([], dtype=torch.int64), 0)
+
+    bs, num_slots = 4, 30  # 7 whole blocks and 2 slots of block 7
+    tables = torch.tensor([[1, 7, 99], [6, 0, -5]], dtype=torch.int32)
+    _native.check_tables("t", tables, torch.tensor([6, 5], dtype=torch.int32), bs, num_slots)
+    # block 7 holds only slots 28, 29: a third token in it is out of the pool
+    with pytest.raises(IndexError, match="column 1"):
+        _native.check_tables("t", tables, torch.tensor([7, 5], dtype=torch.int32), bs, num_slots)
+    # column 2 (id 99) becomes used
+    with pytest.raises(IndexError, match="sequence 0 column 2"):
+        _native.check_tables("t", torch.tensor([[1, 2, 99], [6, 0, -5]], dtype=torch.int32),
+                             torch.tensor([9, 5], dtype=torch.int32), bs, num_slots)  # fmt: skip
+    # negative id in a used column
+    with pytest.raises(IndexError, match="sequence 1 column 2"):
+        _native.check_tables("t", tables, torch.tensor([2, 9], dtype=torch.int32), bs, num_slots)
+    # a context longer than the table covers, or negative
+    for n in (13, -1):
+        with pytest.raises(IndexError, match="context_lens"):
+            _native.check_tables("t", tables, torch.tensor([n, 1], dtype=torch.int32), bs,
+                                 num_slots)  # fmt: skip
+    # first= skips the leading columns (the cascade tail reads from there on)
+    _native.check_tables("t", tables[:, 1:].contiguous(), torch.tensor([2, 1], dtype=torch.int32),
+                         bs, num_slots)  # fmt: skip
+    _native.check_tables("t", tables, torch.tensor([2, 1], dtype=torch.int32), bs, num_slots,
+                         first=1)  # fmt: skip
+
+
+def test_debug_checks_switch():
+    prev = _native.set_debug_checks(True)
+    try:
+        assert _native.debug_checks()
+        assert _native.set_debug_checks(False) is True
+        assert not _native.debug_checks()
+    finally:
+        _native.set_debug_checks(prev)

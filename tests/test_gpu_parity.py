@@ -123,6 +123,51 @@ def test_append_edge_cases():
         kv_append(kp, vp, k, v, torch.tensor([1, 2, 3], device=DEV))
 
 
+
+def test_debug_checks_raise_like_the_reference():
+    """With the opt-in metadata checks on, metadata the kernels would skip or mask
+    raises IndexError before any launch (index_copy_ and the reference's gather raise
+    there), nothing is written, and good metadata still gives the unchecked results."""
+    _say("debug checks")
+    step = workloads.custom([50, 300, 7], 8, 2, 64, 16, torch.bfloat16, DEV, seed=3)
+    args = (step.q, step.k_cache, step.v_cache, step.block_tables, step.context_lens, 16)
+    plain = pa.paged_decode_attention(*args)
+    prev = _native.set_debug_checks(True)
+    try:
+        kp = torch.zeros(32, 2, 16, dtype=torch.bfloat16, device=DEV)
+        vp = torch.zeros_like(kp)
+        k = torch.randn(2, 2, 16, device=DEV).to(torch.bfloat16)
+        with pytest.raises(IndexError, match="outside the pool"):
+            kv_append(kp, vp, k, k, torch.tensor([5, 32], device=DEV))
+        torch.cuda.synchronize()
+        assert not kp.any()
+        kv_append(kp, vp, k, k, torch.tensor([5, 31], device=DEV))
+        torch.cuda.synchronize()
+        assert torch.equal(kp[31], k[1])
+        assert torch.equal(pa.paged_decode_attention(*args), plain)
+        nblk = step.k_cache.shape[0] // 16
+        bad = step.block_tables.clone()
+        bad[1, 3] = nblk  # a used column of sequence 1 (300 tokens)
+        with pytest.raises(IndexError, match="sequence 1 column 3"):
+            pa.paged_decode_attention(step.q, step.k_cache, step.v_cache, bad,
+                                      step.context_lens, 16)  # fmt: skip
+        long_ctx = step.context_lens.clone()
+        long_ctx[0] = step.block_tables.shape[1] * 16 + 1
+        with pytest.raises(IndexError, match="context_lens"):
+            pa.paged_decode_attention(step.q, step.k_cache, step.v_cache, step.block_tables,
+                                      long_ctx, 16)  # fmt: skip
+        with pytest.raises(IndexError, match="outside the pool"):
+            copy_blocks(step.k_cache, step.v_cache,
+                        torch.tensor([[0, nblk]], device=DEV), 16)  # fmt: skip
+        cu = torch.tensor([0, 3, 2], dtype=torch.int32, device=DEV)
+        q_rows = torch.randn(3, 8, 64, device=DEV).to(torch.bfloat16)
+        with pytest.raises(IndexError, match="cu_seqlens_q"):
+            pa.paged_prefill_attention(q_rows, step.k_cache, step.v_cache,
+                                       step.block_tables[:2].contiguous(),
+                                       step.context_lens[:2].contiguous(), 16, cu, 3)  # fmt: skip
+    finally:
+        _native.set_debug_checks(prev)
+
 def test_paged_cache_write_all_layers():
     _say("PagedKVCache.write")
     cfg = KVShape(num_hidden_layers=3, num_key_value_heads=8, head_dim=128)
