@@ -243,7 +243,8 @@ int pkv_paged_prefill(void* out, int out_dtype, int64_t out_stride_tok, int64_t 
  *     shared prefix), instead of the bottom-right causal limit;
  *   q_rows (int32 [tokens], or NULL = identity): query token t of the step reads q row
  *     q_rows[t] (a chunk's queries can be rows scattered over the batch); out and lse
- *     stay in step order;
+ *     stay in step order; a negative q_rows[t] means no query at t: nothing is read
+ *     for it and its out and lse rows are left untouched (padding in a fixed layout);
  *   lse (fp32 [tokens, num_heads], or NULL): log2 normalisers as in pkv_paged_decode_ex.
  */
 int pkv_paged_prefill_ex(void* out, int out_dtype, int64_t out_stride_tok, int64_t out_stride_h,

@@ -262,7 +262,12 @@ paged_prefill_kernel(const PrefillArgs a) {
     row_ok[t] = rho < nrows;
     const int rr = row_ok[t] ? rho : 0;
     row_tok[t] = rr / G;
-    const int64_t qrow = a.q_rows ? a.q_rows[q0 + row_tok[t]] : q0 + row_tok[t];
+    int64_t qrow = q0 + row_tok[t];
+    if (a.q_rows) {  // a negative entry: no query there (nothing read or written)
+      const int qr = a.q_rows[q0 + row_tok[t]];
+      row_ok[t] = row_ok[t] && qr >= 0;
+      qrow = qr >= 0 ? qr : 0;
+    }
     const S* qp = reinterpret_cast<const S*>(a.q) + qrow * a.q_st +
                   (int64_t)(kvh * G + rr % G) * a.q_sh + 8 * grp;
 #pragma unroll
@@ -750,11 +755,10 @@ paged_prefill_rows_kernel(const PrefillArgs a) {
     const int p = e / HD, d = e - p * HD;
     const int i = tok0 + p / GPW, h = h0 + p % GPW;
     float x = 0.f;
-    if (i < ql && h < hend) {
-      const int row = a.q_rows ? a.q_rows[q0 + i] : q0 + i;
+    const int row = i < ql ? (a.q_rows ? a.q_rows[q0 + i] : q0 + i) : -1;
+    if (row >= 0 && h < hend)  // a negative q_rows entry: no query there
       x = Elt<DT>::to_f32(reinterpret_cast<const S*>(a.q)[(int64_t)row * a.q_st +
                                                         (int64_t)h * a.q_sh + d]);
-    }
     qs[wave][p][d] = x * a.scale_log2;
   }
   int qpos[TPW];  // position of each token of the wave (keys <= qpos are visible)
@@ -862,7 +866,7 @@ paged_prefill_rows_kernel(const PrefillArgs a) {
   for (int p = 0; p < P; ++p) {
     const float lt = across_sum_exact<1>(l[p]);
     const int i = tok0 + p / GPW, h = h0 + p % GPW;
-    if (i >= ql || h >= hend) continue;
+    if (i >= ql || h >= hend || (a.q_rows && a.q_rows[q0 + i] < 0)) continue;
     const float inv = lt > 0.f ? 1.f / lt : 0.f;  // nothing visible: 0
     const int64_t t = q0 + i;
 #pragma unroll

@@ -25,6 +25,7 @@ from __future__ import annotations
 from collections.abc import Sequence
 from dataclasses import dataclass
 
+import numpy as np
 import torch
 
 from engine.kernels import _native
@@ -134,80 +135,161 @@ class PrefixGroups:
     max_members: int
 
 
+def shared_prefixes(tables: np.ndarray, context_lens: np.ndarray, block_size: int,
+                    min_blocks: int = 16) -> list[tuple[np.ndarray, int]]:  # fmt: skip
+    """Groups of a decode batch's sequences that start with the same physical blocks, as
+    (members ascending, shared blocks) in order of first block id.
+
+    Sequences whose first block is the same form a group (at least two members); its
+    shared prefix is the longest run of leading blocks every member's table holds and
+    every member's context covers completely, kept if at least ``min_blocks`` long.
+    tables: int [B, W]; context_lens: int [B] (host arrays)."""
+    tables = np.asarray(tables)
+    b, w = tables.shape
+    full = np.minimum(np.asarray(context_lens, dtype=np.int64) // block_size, w)
+    eligible = full >= min_blocks
+    if w == 0 or int(eligible.sum()) < 2:
+        return []
+    firsts = np.where(eligible, tables[:, 0].astype(np.int64), -1)
+    order = np.argsort(firsts, kind="stable")
+    ranked = firsts[order]
+    starts = np.flatnonzero(np.r_[True, ranked[1:] != ranked[:-1]])
+    groups = []
+    for lo, hi in zip(starts, np.r_[starts[1:], b], strict=True):
+        if ranked[lo] < 0 or hi - lo < 2:
+            continue
+        members = order[lo:hi]  # stable sort: already ascending
+        rows = tables[members]
+        lcp = np.cumprod(rows == rows[:1], axis=1).sum(1)
+        shared = int(np.minimum(lcp, full[members]).min())
+        if shared >= min_blocks:
+            groups.append((members, shared))
+    return groups
+
+
 def find_prefix_groups(block_tables: Sequence[Sequence[int]] | torch.Tensor,
                        context_lens: Sequence[int] | torch.Tensor, block_size: int,
                        num_heads: int, num_kv_heads: int, device: torch.device, *,
                        min_blocks: int = 16, target_workgroups: int | None = None,
                        pieces: int | None = None) -> PrefixGroups | None:  # fmt: skip
-    """Group the sequences of a decode batch that start with the same physical blocks.
-
-    Sequences whose first block is the same form a group (at least two members); its
-    shared prefix is the longest run of leading blocks every member's table holds and
-    every member's context covers completely, if it is at least ``min_blocks`` long.
-    Host-side (the tables the engine's block manager produced); returns None when no
-    group qualifies. Each prefix is cut into K pieces (K >= 1, pieces of at least 4
-    blocks), K = ``pieces`` if given, else the most whose prefix pass has at most
+    """The ``shared_prefixes`` groups of a decode batch laid out for cascade decode
+    (host-side, from the tables the engine's block manager produced); None when no group
+    qualifies. Each prefix is cut into K pieces (K >= 1, pieces of at least 4 blocks),
+    K = ``pieces`` if given, else the most whose prefix pass has at most
     ``target_workgroups`` workgroups (default: the GPU's CU count, one workgroup per
     CU -- a second per CU shares the same matrix cores and only adds parts to merge)."""
-    tables = torch.as_tensor(block_tables, dtype=torch.int32).cpu()
-    ctx = torch.as_tensor(context_lens, dtype=torch.int64).cpu()
-    b, w = tables.shape
-    full = torch.clamp(ctx // block_size, max=w)
-    groups: list[tuple[torch.Tensor, int]] = []
-    eligible = full >= min_blocks
-    if w and int(eligible.sum()) >= 2:
-        firsts = tables[:, 0].clone()
-        firsts[~eligible] = -1
-        ids, counts = torch.unique(firsts, return_counts=True)
-        for fid, cnt in zip(ids.tolist(), counts.tolist(), strict=True):
-            if fid < 0 or cnt < 2:
-                continue
-            members = torch.nonzero(firsts == fid).flatten()
-            rows = tables[members]
-            lcp = (rows == rows[:1]).int().cumprod(1).sum(1)
-            shared = int(torch.minimum(lcp, full[members]).min())
-            if shared >= min_blocks:
-                groups.append((members, shared))
+    tables = torch.as_tensor(block_tables, dtype=torch.int32).cpu().numpy()
+    ctx = torch.as_tensor(context_lens, dtype=torch.int64).cpu().numpy()
+    groups = shared_prefixes(tables, ctx, block_size, min_blocks)
     if not groups:
         return None
+    b = tables.shape[0]
     g_count = len(groups)
     sizes = [len(m) for m, _ in groups]
     s_total = sum(sizes)
     max_members = max(sizes)
-    groups_rows = -(-max_members * (num_heads // num_kv_heads) // 128)
-    per_piece = max(1, groups_rows * num_kv_heads * g_count)
-    min_shared = min(sh for _, sh in groups)
     dev = torch.device(device)
     if pieces is None:
         if target_workgroups is None:
-            target_workgroups = torch.cuda.get_device_properties(dev).multi_processor_count \
-                if dev.type == "cuda" else 256  # fmt: skip
-        pieces = target_workgroups // per_piece
-    pieces = max(1, min(pieces, min_shared // 4))
-    first_block = torch.zeros(b, dtype=torch.int32)
-    prefix_row = torch.full((b,), -1, dtype=torch.int32)
-    order = torch.cat([m for m, _ in groups]).to(torch.int32)
-    cu = [0]
-    for (members, shared), size in zip(groups, sizes, strict=True):
-        first_block[members] = shared
-        prefix_row[members] = torch.arange(cu[-1], cu[-1] + size, dtype=torch.int32)
-        cu.append(cu[-1] + size)
-    piece_blocks = [-(-shared // pieces) for _, shared in groups]
-    width = max(max(piece_blocks), 1)
-    ptables = torch.zeros(pieces * g_count, width, dtype=torch.int32)
-    pctx = torch.zeros(pieces * g_count, dtype=torch.int32)
-    cu_q = torch.zeros(pieces * g_count + 1, dtype=torch.int32)
-    for k in range(pieces):
-        for g, ((members, shared), pb) in enumerate(zip(groups, piece_blocks, strict=True)):
-            c = k * g_count + g
+            target_workgroups = _cu_count(dev)
+        per_piece = _prefix_workgroups(max_members, num_heads // num_kv_heads, num_kv_heads)
+        pieces = target_workgroups // (per_piece * g_count)
+    pieces = max(1, min(pieces, min(sh for _, sh in groups) // 4))
+    width = max(-(-shared // pieces) for _, shared in groups)
+    host = np.zeros(_prefix_entries(b, pieces, g_count, width, s_total), dtype=np.int32)
+    _fill_prefix(host, b, pieces, g_count, width, tables, groups, block_size, s_total)
+    return _prefix_view(torch.from_numpy(host).to(dev), b, pieces, g_count, width,
+                        members=s_total, max_members=max_members)  # fmt: skip
+
+
+def _cu_count(dev: torch.device) -> int:
+    return torch.cuda.get_device_properties(dev).multi_processor_count \
+        if dev.type == "cuda" else 256  # fmt: skip
+
+
+def _prefix_workgroups(members: int, groups: int, num_kv_heads: int) -> int:
+    """Workgroups of one prefix piece of a group: 128 query rows (member x query head of
+    one KV head) per workgroup, for every KV head."""
+    return max(1, -(-members * groups // 128) * num_kv_heads)
+
+
+def cascade_pieces(batch: int, num_heads: int, num_kv_heads: int, device: torch.device,
+                   max_pieces: int = 8) -> int:  # fmt: skip
+    """Pieces per shared prefix for a captured step of ``batch`` sequences: as many as
+    keep one group's prefix pass within one workgroup per CU (at most ``max_pieces``)."""
+    per_piece = _prefix_workgroups(batch, num_heads // num_kv_heads, num_kv_heads)
+    return max(1, min(max_pieces, _cu_count(torch.device(device)) // per_piece))
+
+
+# Layout of prefix groups in one int32 array, for a batch of n sequences, K pieces, C
+# chunks per piece, piece tables W' wide and member rows S apart between pieces:
+# first_block [n] | prefix_row [n] | q_rows [K S] | cu_q [K C + 1] | ctx [K C] |
+# tables [K C, W']. Part k of grouped sequence b is row prefix_row[b] + k S of the
+# prefix pass.
+def _prefix_entries(n: int, pieces: int, slots: int, width: int, stride: int) -> int:
+    chunks = pieces * slots
+    return 2 * n + pieces * stride + 2 * chunks + 1 + chunks * width
+
+
+def _prefix_view(flat: torch.Tensor, n: int, pieces: int, groups: int, width: int, *,
+                 members: int, max_members: int) -> PrefixGroups:  # fmt: skip
+    chunks = pieces * groups
+    at = [0]
+
+    def take(count: int) -> torch.Tensor:
+        t = flat[at[0] : at[0] + count]
+        at[0] += count
+        return t
+
+    return PrefixGroups(first_block=take(n), prefix_row=take(n), q_rows=take(pieces * members),
+                        cu_q=take(chunks + 1), ctx=take(chunks),
+                        tables=take(chunks * width).view(chunks, width), members=members,
+                        pieces=pieces, max_members=max_members)  # fmt: skip
+
+
+def _fill_prefix(host: np.ndarray, n: int, pieces: int, slots: int, width: int,
+                 tables: np.ndarray, groups: list[tuple[np.ndarray, int]], block_size: int,
+                 stride: int) -> None:  # fmt: skip
+    """Write ``groups`` into the flat layout above: ``slots`` chunks per piece, the
+    groups' member rows ``stride`` apart between pieces. Sequences outside every group
+    get first_block 0 and prefix_row -1. Rows of a piece past its groups' members (when
+    stride exceeds them) belong to the piece's last chunk, which then must be free of
+    groups; their q_rows entry is -1, so the prefix pass skips them."""
+    used = groups[: slots - 1] if stride > sum(len(m) for m, _ in groups) else groups
+    if len(used) > slots:
+        raise ValueError(f"prefix groups: {len(used)} groups for {slots} chunk slots")
+    chunks = pieces * slots
+    o_pr, o_qr = n, 2 * n
+    o_cu = o_qr + pieces * stride
+    o_ctx = o_cu + chunks + 1
+    o_tab = o_ctx + chunks
+    host[: o_tab + chunks * width] = 0
+    host[o_pr : o_pr + n] = -1
+    host[o_qr : o_qr + pieces * stride] = -1
+    ptab = host[o_tab : o_tab + chunks * width].reshape(chunks, width)
+    ends, row = [], 0
+    for g, (members, shared) in enumerate(used):
+        size = len(members)
+        host[members] = shared  # first_block
+        host[o_pr + members] = np.arange(row, row + size)
+        pb = -(-shared // pieces)
+        for k in range(pieces):
+            host[o_qr + k * stride + row : o_qr + k * stride + row + size] = members
             lo, hi = min(k * pb, shared), min((k + 1) * pb, shared)
-            ptables[c, : hi - lo] = tables[members[0], lo:hi]
-            pctx[c] = (hi - lo) * block_size
-            cu_q[c + 1] = k * s_total + cu[g + 1]
-    return PrefixGroups(
-        first_block=first_block.to(dev), prefix_row=prefix_row.to(dev),
-        q_rows=order.repeat(pieces).to(dev), cu_q=cu_q.to(dev), ctx=pctx.to(dev),
-        tables=ptables.to(dev), members=s_total, pieces=pieces, max_members=max_members)  # fmt: skip
+            c = k * slots + g
+            ptab[c, : hi - lo] = tables[members[0], lo:hi]
+            host[o_ctx + c] = (hi - lo) * block_size
+        row += size
+        ends.append(row)
+    # cu_q: chunk k * slots + g ends at k S + (its group's last row); the free chunks of
+    # a piece are empty but for the last, which runs to the next piece's first row.
+    cu = np.zeros(chunks + 1, dtype=np.int64)
+    for k in range(pieces):
+        for g in range(slots):
+            c = k * slots + g
+            cu[c + 1] = k * stride + (ends[g] if g < len(ends) else row)
+        cu[(k + 1) * slots] = (k + 1) * stride
+    host[o_cu : o_cu + chunks + 1] = cu
 
 
 def paged_decode_attention(

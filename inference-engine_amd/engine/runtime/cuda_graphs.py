@@ -17,6 +17,7 @@ from collections.abc import Callable, Sequence
 import numpy as np
 import torch
 
+from engine.kernels import paged_attention as pa
 from engine.runtime.paged_cache import PagedBatch, PagedKVCache, decode_slots
 
 # Batch-size buckets of decode graphs (the reference's table).
@@ -28,36 +29,66 @@ class DecodeGraphs:
     [n, 1, vocab]`` as one graph per batch bucket n.
 
     Step metadata lives in one int32 device block laid out as
-    ``[ctx (M) | ids (M) | positions (M) | tables (M, W)]`` for the largest bucket M and
-    table width W, so bucket n's data is the contiguous prefix of 3 M + n W entries. A
-    step fills a pinned host copy of that prefix with numpy and sends it with a single
-    asynchronous copy; the captured graph widens ids and positions to int64, builds the
-    slot mapping on the device (``decode_slots``) and runs the model. Padding rows have
-    context length 1 in the scratch block.
+    ``[ctx (M) | ids (M) | positions (M) | prefix groups (P) | tables (M, W)]`` for the
+    largest bucket M and table width W, so bucket n's data is the contiguous prefix of
+    3 M + P + n W entries. A step fills a pinned host copy of that prefix with numpy and
+    sends it with a single asynchronous copy; the captured graph widens ids and
+    positions to int64, builds the slot mapping on the device (``decode_slots``) and runs
+    the model. Padding rows have context length 1 in the scratch block.
+
+    ``cascade`` (needs the model's ``num_heads``): every step also looks for sequences
+    whose tables start with the same blocks (``shared_prefixes``, at least
+    ``cascade_min_blocks``; the ``max_groups`` largest groups) and lays them out in the
+    prefix-groups region in a fixed shape per bucket -- K pieces, max_groups + 1 chunks
+    per piece, member rows n apart -- which the captured decode calls read as their
+    ``prefix_groups``: each shared prefix is read once per layer-step for its whole
+    group. A step without groups runs the plain decode inside the same graph. Every
+    chunk slot adds workgroups to the prefix pass whether a group fills it or not (at
+    config 3, 256 sequences: 129.6 us per layer-step with 1 slot for groups, 136.4 us
+    with 4), hence the default of 2 groups.
     """
 
     def __init__(self, model: Callable, cache: PagedKVCache, scratch_block: int,
-                 max_batch: int, max_blocks_per_seq: int) -> None:  # fmt: skip
+                 max_batch: int, max_blocks_per_seq: int, *, cascade: bool = False,
+                 num_heads: int | None = None, cascade_min_blocks: int = 16,
+                 max_groups: int = 2) -> None:  # fmt: skip
         if max_batch < 1 or max_blocks_per_seq < 1:
             raise ValueError("DecodeGraphs: max_batch and max_blocks_per_seq must be >= 1")
+        if cascade and not num_heads:
+            raise ValueError("DecodeGraphs: cascade needs the model's num_heads")
         self.model, self.cache, self.scratch_block = model, cache, scratch_block
         self.sizes = sorted({s for s in BUCKETS if s < max_batch} | {max_batch})
         self.max_width = max_blocks_per_seq
         top, w = self.sizes[-1], max_blocks_per_seq
         dev = cache.k.device
-        self._host = torch.zeros(3 * top + top * w, dtype=torch.int32, pin_memory=True)
+        self.cascade, self.min_blocks, self.max_groups = cascade, cascade_min_blocks, max_groups
+        # Per bucket: (pieces, chunk slots per piece, piece table width) of its layout.
+        self._shape: dict[int, tuple[int, int, int]] = {}
+        pre = 0
+        if cascade:
+            nkv = cache.k.shape[2]
+            for n in self.sizes:
+                k = pa.cascade_pieces(n, num_heads, nkv, dev)
+                self._shape[n] = (k, max_groups + 1, -(-w // k))
+                pre = max(pre, pa._prefix_entries(n, *self._shape[n], n))
+        self._pre_len = pre
+        self._host = torch.zeros(3 * top + pre + top * w, dtype=torch.int32, pin_memory=True)
         self._meta = torch.zeros_like(self._host, device=dev)
         h = self._host.numpy()
         self._h_ctx, self._h_ids, self._h_pos = h[:top], h[top : 2 * top], h[2 * top : 3 * top]
-        self._h_tab = h[3 * top :].reshape(top, w)
+        self._h_pre = h[3 * top : 3 * top + pre]
+        self._h_tab = h[3 * top + pre :].reshape(top, w)
         self._ctx, self._ids = self._meta[:top], self._meta[top : 2 * top]
-        self._pos, self._tab = self._meta[2 * top : 3 * top], self._meta[3 * top :].view(top, w)
+        self._pos = self._meta[2 * top : 3 * top]
+        self._pre = self._meta[3 * top : 3 * top + pre]
+        self._tab = self._meta[3 * top + pre :].view(top, w)
         self._slots = torch.empty(top, dtype=torch.int64, device=dev)
         self._sent = torch.cuda.Event()  # the host block may be rewritten once this fires
         self._sent.record()
         self._graphs: dict[int, torch.cuda.CUDAGraph] = {}
         self._logits: dict[int, torch.Tensor] = {}
         self._batches = {n: self._batch_of(n) for n in self.sizes}
+        self.groups_last_step = 0
         self._stage(top, [], [], [], [])  # an all-padding step for the warm-up
         self._meta.copy_(self._host)
         pool = torch.cuda.graph_pool_handle()
@@ -78,10 +109,15 @@ class DecodeGraphs:
         """The decode batch of bucket n, all of whose tensors are views of the static
         buffers (the graph reads them by address)."""
         flat = torch.arange(n, device=self._meta.device)
-        return PagedBatch(cache=self.cache, slot_mapping=self._slots[:n], kv_slots=flat,
-                          q_index=flat[:, None], q_valid=torch.ones_like(flat[:, None], dtype=torch.bool),
-                          attn_mask=None, last_index=flat, use_kernel=True,
-                          block_tables=self._tab[:n], context_lens=self._ctx[:n])  # fmt: skip
+        batch = PagedBatch(cache=self.cache, slot_mapping=self._slots[:n], kv_slots=flat,
+                           q_index=flat[:, None], q_valid=torch.ones_like(flat[:, None], dtype=torch.bool),
+                           attn_mask=None, last_index=flat, use_kernel=True,
+                           block_tables=self._tab[:n], context_lens=self._ctx[:n])  # fmt: skip
+        if self.cascade:
+            k, slots, width = self._shape[n]
+            batch.prefix_groups = pa._prefix_view(self._pre, n, k, slots, width, members=n,
+                                                  max_members=n)  # fmt: skip
+        return batch
 
     def _forward(self, n: int) -> torch.Tensor:
         batch = self._batches[n]
@@ -105,6 +141,17 @@ class DecodeGraphs:
         self._h_tab[b:n, 0] = self.scratch_block
         for r, row in enumerate(tables):
             self._h_tab[r, : len(row)] = row
+        if self.cascade:
+            k, slots, width = self._shape[n]
+            groups = pa.shared_prefixes(self._h_tab[:b], self._h_ctx[:b], self.cache.block_size,
+                                        self.min_blocks) if b else []  # fmt: skip
+            # the largest first: a step with more groups than chunk slots leaves the
+            # smallest ones to the plain decode
+            groups.sort(key=lambda g: -len(g[0]) * g[1])
+            groups = groups[: slots - 1]
+            pa._fill_prefix(self._h_pre, n, k, slots, width, self._h_tab, groups,
+                            self.cache.block_size, n)  # fmt: skip
+            self.groups_last_step = len(groups)
 
     def can_run(self, batch_size: int, width: int) -> bool:
         return batch_size <= self.sizes[-1] and width <= self.max_width
@@ -124,7 +171,7 @@ class DecodeGraphs:
         n = self.sizes[bisect.bisect_left(self.sizes, b)]
         self._stage(n, np.asarray(ids), np.asarray(positions), tables, np.asarray(context_lens))
         top = self.sizes[-1]
-        used = 3 * top + n * self.max_width
+        used = 3 * top + self._pre_len + n * self.max_width
         self._meta[:used].copy_(self._host[:used], non_blocking=True)
         self._sent.record()
         self._graphs[n].replay()

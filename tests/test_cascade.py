@@ -155,3 +155,156 @@ def test_cascade_many_parts_and_pieces(wgs):
     torch.cuda.synchronize()
     want = oracle.decode_attention(q, k, v, tables, ctx, 16, threads=THREADS)
     assert (got.cpu() - want).abs().max().item() <= 2e-3
+
+
+def _static_layout(n, pieces, slots, width, tables, ctx, bs, min_blocks, groups=None):
+    """The fixed-shape layout a captured decode step reads (stride n, `slots` chunks per
+    piece), filled on the host for one step's tables: (flat int32 array, groups used)."""
+    import numpy as np
+
+    flat = np.zeros(pa._prefix_entries(n, pieces, slots, width, n), dtype=np.int32)
+    tab = np.zeros((n, tables.shape[1]), dtype=np.int32)
+    tab[: tables.shape[0]] = tables.numpy()
+    if groups is None:
+        groups = pa.shared_prefixes(tab[: tables.shape[0]], ctx.numpy(), bs, min_blocks)
+    groups = groups[: slots - 1]
+    pa._fill_prefix(flat, n, pieces, slots, width, tab, groups, bs, n)
+    return flat, groups
+
+
+def test_static_prefix_layout_covers_every_context_exactly():
+    """The fixed layout of a graph bucket (n rows apart between pieces, one more chunk
+    slot per piece than groups): every grouped sequence's prefix pieces plus its tail
+    visit exactly its own slots; rows past the groups' members sit in the piece's last
+    chunk, have no keys and q_rows -1; padding rows and ungrouped sequences get no
+    prefix; cu_q never decreases and ends at pieces * n."""
+    import numpy as np
+
+    bs = 16
+    t1, c1, _ = _shared_batch(b=10, shared_blocks=12, tails=[3, 0, 40, 17, 1, 16, 9, 2, 5, 7],
+                              extra=3, seed=4)  # fmt: skip
+    t2, c2, _ = _shared_batch(b=6, shared_blocks=9, tails=[1, 2, 3, 4, 5, 6], extra=1, seed=5)
+    t2 = t2 + 1000  # a second group on other blocks
+    w = max(t1.shape[1], t2.shape[1])
+    tables = torch.zeros(16, w, dtype=torch.int32)
+    tables[:10, : t1.shape[1]] = t1
+    tables[10:16, : t2.shape[1]] = t2
+    ctx = torch.cat([c1, c2])
+    n, pieces, slots = 24, 3, 4  # bucket 24 for 16 sequences
+    width = -(-w // pieces)
+    for min_blocks in (4, 10, 100):
+        flat, groups = _static_layout(n, pieces, slots, width, tables, ctx, bs, min_blocks)
+        pg = pa._prefix_view(torch.from_numpy(flat), n, pieces, slots, width, members=n,
+                             max_members=n)  # fmt: skip
+        assert len(groups) == {4: 2, 10: 1, 100: 0}[min_blocks]
+        cu = pg.cu_q.tolist()
+        assert cu[0] == 0 and cu[-1] == pieces * n and all(a <= b for a, b in zip(cu, cu[1:]))
+        chunk_of = np.searchsorted(np.asarray(cu), np.arange(pieces * n), side="right") - 1
+        members = sum(len(m) for m, _ in groups)
+        for k in range(pieces):
+            for r in range(members, n):  # rows past the members: skipped, no keys
+                row = k * n + r
+                assert int(pg.q_rows[row]) == -1 and int(pg.ctx[chunk_of[row]]) == 0
+        for b in range(n):
+            r = int(pg.prefix_row[b])
+            fb = int(pg.first_block[b])
+            if b >= 16:  # padding rows
+                assert r == -1 and fb == 0
+                continue
+            seqn = int(ctx[b])
+            own = [int(tables[b, p // bs]) * bs + p % bs for p in range(seqn)]
+            seen = []
+            if r >= 0:
+                for k in range(pieces):
+                    row = r + k * n
+                    c = chunk_of[row]
+                    assert int(pg.q_rows[row]) == b
+                    seen += [int(pg.tables[c, p // bs]) * bs + p % bs for p in range(int(pg.ctx[c]))]
+            assert (r >= 0) == (fb > 0)
+            seen += [int(tables[b, fb + p // bs]) * bs + p % bs for p in range(seqn - fb * bs)]
+            assert seen == own, (min_blocks, b)
+
+
+@pytest.mark.gpu
+def test_cascade_static_layout_graph_replays_match_oracle():
+    """One captured decode call with fixed-shape prefix groups (what DecodeGraphs holds
+    per bucket), replayed over steps whose metadata is rewritten in place: config 3 in
+    full (one group of 256), the same batch with no group (plain decode inside the
+    graph), and a smaller batch padded to the bucket with two groups -- each replay
+    against the oracle, bit-identical replays of one step."""
+    import numpy as np
+
+    from engine import workloads
+    from engine.runtime.paged_cache import copy_blocks, kv_append
+    from oracle import oracle
+
+    dev = torch.device("cuda:0")
+    step = workloads.config3(dev, seed=0)
+    copy_blocks(step.k_cache, step.v_cache, step.cow_mapping, step.block_size)
+    kv_append(step.k_cache, step.v_cache, step.new_k, step.new_v, step.slot_mapping)
+    n, nh, hd = step.q.shape
+    nkv, bs, w = step.k_cache.shape[1], step.block_size, step.block_tables.shape[1]
+    pieces = pa.cascade_pieces(n, nh, nkv, dev)
+    slots, width = 3, -(-w // pieces)
+    meta = torch.zeros(pa._prefix_entries(n, pieces, slots, width, n), dtype=torch.int32,
+                       device=dev)  # fmt: skip
+    tables = torch.zeros(n, w, dtype=torch.int32, device=dev)
+    ctx = torch.ones(n, dtype=torch.int32, device=dev)
+    q = step.q.clone()
+    out = torch.empty(n, nh, hd, dtype=torch.float32, device=dev)
+    pg = pa._prefix_view(meta, n, pieces, slots, width, members=n, max_members=n)
+
+    def call():
+        pa.paged_decode_attention(q, step.k_cache, step.v_cache, tables, ctx, bs, out=out,
+                                  prefix_groups=pg)  # fmt: skip
+
+    def load(tab, cx, qq, min_blocks):
+        b = tab.shape[0]
+        flat, groups = _static_layout(n, pieces, slots, width, tab, cx, bs, min_blocks)
+        meta.copy_(torch.from_numpy(flat))
+        tables.zero_()
+        tables[:b] = tab.to(dev)
+        ctx.fill_(1)
+        ctx[:b] = cx.to(dev)
+        q[:b] = qq
+        return groups
+
+    load(step.block_tables.cpu(), step.context_lens.cpu(), step.q, 16)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        call()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call()
+
+    # a smaller batch: sequences 0-99 keep the group, 100-179 move to a second group on
+    # copies of the prefix blocks, padded to 256 rows
+    small_tab = step.block_tables[:180].cpu().clone()
+    used = set(step.block_tables.flatten().tolist()) | set(step.cow_mapping.flatten().tolist())
+    free = torch.tensor([x for x in range(step.k_cache.shape[0] // bs) if x not in used][:127],
+                        dtype=torch.int64)  # fmt: skip
+    assert free.numel() == 127
+    pairs = torch.stack([step.block_tables[150, :127].long().cpu(), free], 1).to(dev)
+    copy_blocks(step.k_cache, step.v_cache, pairs, bs)
+    small_tab[100:180, :127] = free.to(torch.int32)
+    cases = [("config 3, one group", step.block_tables.cpu(), step.context_lens.cpu(), 16, 1),
+             ("config 3, no group", step.block_tables.cpu(), step.context_lens.cpu(), 10**6, 0),
+             ("180 of 256 rows, two groups", small_tab, step.context_lens[:180].cpu(), 16, 2)]
+    kc, vc = step.k_cache.cpu(), step.v_cache.cpu()
+    for name, tab, cx, min_blocks, n_groups in cases:
+        print("[case]", name, flush=True)
+        groups = load(tab, cx, step.q[: tab.shape[0]], min_blocks)
+        assert len(groups) == n_groups
+        graph.replay()
+        torch.cuda.synchronize()
+        first = out.clone()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, first), name
+        b = tab.shape[0]
+        want = oracle.decode_attention(step.q[:b].cpu(), kc, vc, tab, cx, bs, threads=THREADS)
+        err = (out[:b].cpu() - want).abs().max().item()
+        assert err <= 2e-3, (name, err)
+        assert np.isfinite(out.cpu().numpy()).all(), name

@@ -248,6 +248,33 @@ def test_engine_cascade_decode_matches_plain(dtype):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_decode_graphs_cascade_matches_plain(dtype):
+    """Decode steps replayed from hipGraphs with cascade on: each step's prefix groups
+    are laid out in the graphs' static buffers (groups come and go between replays of
+    one graph, and steps without any run the plain decode inside it). Same tokens as the
+    eager plain decode, logits within 16-bit rounding."""
+    from tiny_llama import KernelBackend
+
+    model = _cuda_model(dtype)
+    prompts = {"b": SHARED + [1, 2], "d": SHARED + [3], "a": [5, 6, 7], "f": SHARED,
+               "g": SHARED + [4, 5, 6]}  # fmt: skip
+    runs = {}
+    for graphs, min_blocks in ((False, None), (True, 2)):
+        eng = TinyEngine(model, KernelBackend(), num_blocks=64, block_size=4, max_num_seqs=8,
+                         graphs=graphs, cascade_min_blocks=min_blocks)  # fmt: skip
+        runs[graphs] = (_run_staggered(eng, prompts, 12), eng)
+    log = runs[True][1].log
+    assert any(s["graph"] and s["cascade"] for s in log)
+    assert runs[True][0] == runs[False][0]
+    worst = max((torch.stack(runs[True][1].logits[r]) -
+                 torch.stack(runs[False][1].logits[r])).abs().max().item()
+                for r in prompts)  # fmt: skip
+    assert worst <= 0.05, worst
+    assert runs[True][1].bm.num_free_blocks == 64
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_decode_graphs_match_eager(dtype):
     """Decode steps replayed from hipGraphs (slot mapping built on the device, padding

@@ -301,7 +301,8 @@ class TinyEngine:
         self.prefix_hits = 0  # admitted prompts that forked another sequence's blocks
         self.max_num_seqs, self.budget = max_num_seqs, max_num_batched_tokens
         self.debug_checks = debug_checks
-        # eager decode steps: cascade over prefixes of at least this many shared blocks
+        # decode steps (eager, and graphs when on): cascade over prefixes of at least this
+        # many shared blocks
         self.cascade_min_blocks = cascade_min_blocks
         self.waiting: list[Seq] = []
         self.running: list[Seq] = []
@@ -314,8 +315,10 @@ class TinyEngine:
         if graphs:
             from engine.runtime.cuda_graphs import DecodeGraphs
 
-            self.graphs = DecodeGraphs(model, self.cache, num_blocks, max_num_seqs,
-                                       num_blocks)  # fmt: skip
+            self.graphs = DecodeGraphs(
+                model, self.cache, num_blocks, max_num_seqs, num_blocks,
+                cascade=cascade_min_blocks is not None, num_heads=cfg.num_attention_heads,
+                cascade_min_blocks=cascade_min_blocks or 16)  # fmt: skip
         self.mixed_graphs = None
         if mixed_graphs:
             from engine.runtime.cuda_graphs import MixedGraphs
@@ -440,7 +443,10 @@ class TinyEngine:
                 self.done[seq.rid] = seq.out
         if self.debug_checks:
             self.bm.check_no_leaks()
-        cascaded = not (used_graph or used_mixed_graph) and batch.prefix_groups is not None
+        if used_graph:
+            cascaded = self.graphs.groups_last_step > 0
+        else:
+            cascaded = not used_mixed_graph and batch.prefix_groups is not None
         self.log.append({"seqs": len(plan), "tokens": len(ids), "decode_only": decode_only,
                          "graph": used_graph, "mixed_graph": used_mixed_graph,
                          "copies": len(pairs), "cascade": cascaded})  # fmt: skip
