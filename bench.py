@@ -307,26 +307,39 @@ def bench_decode(args, torch) -> dict:
 
 
 def bench_cascade(args, torch, step, pools, out, wgs, unique_bytes) -> dict:
-    """The same layer-steps with cascade decode: prefix groups found from the block
-    tables (once per step, on the host), each shared prefix read once per group."""
+    """The same layer-steps with cascade decode as the engine's decode graphs run it:
+    prefix groups found from the block tables on the host, laid out in the graphs'
+    fixed shape (2 group slots, pieces for the batch size), each shared prefix read once
+    per group; timed as hipGraph replays."""
+    import numpy as np
+
     from engine.kernels import paged_attention as pa
 
-    nh, nkv = step.q.shape[1], step.k_cache.shape[1]
-    pg = pa.find_prefix_groups(step.block_tables.cpu(), step.context_lens.cpu(),
-                               step.block_size, nh, nkv, step.q.device)  # fmt: skip
-    if pg is None:
+    n, nh = step.q.shape[0], step.q.shape[1]
+    nkv, bs, w = step.k_cache.shape[1], step.block_size, step.block_tables.shape[1]
+    tables = step.block_tables.cpu().numpy()
+    groups = pa.shared_prefixes(tables, step.context_lens.cpu().numpy(), bs)
+    if not groups:
         return {"cascade": None}
+    pieces, slots = pa.cascade_pieces(n, nh, nkv, step.q.device), 3
+    width = -(-w // pieces)
+    flat = np.zeros(pa.prefix_entries(n, pieces, slots, width, n), dtype=np.int32)
+    groups.sort(key=lambda g: -len(g[0]) * g[1])
+    pa.fill_prefix(flat, n, pieces, slots, width, tables, groups[: slots - 1], bs, n)
+    pg = pa.prefix_view(torch.from_numpy(flat).to(step.q.device), n, pieces, slots, width,
+                        members=n, max_members=n)  # fmt: skip
 
     def fn(k, v):
         return lambda: pa.paged_decode_attention(
-            step.q, k, v, step.block_tables, step.context_lens, step.block_size, out=out,
+            step.q, k, v, step.block_tables, step.context_lens, bs, out=out,
             num_workgroups=wgs, prefix_groups=pg)  # fmt: skip
 
     us = graph_us(torch, [fn(k, v) for k, v in pools], args.steps, args.warmup)[0]
     gbps = unique_bytes / (us * 1e-6) / 1e9
     return {"cascade_us": round(us, 2), "cascade_unique_gbps": round(gbps, 1),
             "cascade_unique_frac": round(gbps / HBM_PEAK_GBPS, 4),
-            "cascade_groups": int(pg.ctx.numel() // pg.pieces), "cascade_pieces": pg.pieces}
+            "cascade_groups": min(len(groups), slots - 1), "cascade_pieces": pieces,
+            "cascade_layout": f"decode-graph fixed shape: {slots - 1} group slots"}
 
 
 def bench_cow(torch, step, layers: int = 28, blocks: int = 2048) -> dict:

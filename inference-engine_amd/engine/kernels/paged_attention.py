@@ -196,9 +196,9 @@ def find_prefix_groups(block_tables: Sequence[Sequence[int]] | torch.Tensor,
         pieces = target_workgroups // (per_piece * g_count)
     pieces = max(1, min(pieces, min(sh for _, sh in groups) // 4))
     width = max(-(-shared // pieces) for _, shared in groups)
-    host = np.zeros(_prefix_entries(b, pieces, g_count, width, s_total), dtype=np.int32)
-    _fill_prefix(host, b, pieces, g_count, width, tables, groups, block_size, s_total)
-    return _prefix_view(torch.from_numpy(host).to(dev), b, pieces, g_count, width,
+    host = np.zeros(prefix_entries(b, pieces, g_count, width, s_total), dtype=np.int32)
+    fill_prefix(host, b, pieces, g_count, width, tables, groups, block_size, s_total)
+    return prefix_view(torch.from_numpy(host).to(dev), b, pieces, g_count, width,
                         members=s_total, max_members=max_members)  # fmt: skip
 
 
@@ -226,12 +226,12 @@ def cascade_pieces(batch: int, num_heads: int, num_kv_heads: int, device: torch.
 # first_block [n] | prefix_row [n] | q_rows [K S] | cu_q [K C + 1] | ctx [K C] |
 # tables [K C, W']. Part k of grouped sequence b is row prefix_row[b] + k S of the
 # prefix pass.
-def _prefix_entries(n: int, pieces: int, slots: int, width: int, stride: int) -> int:
+def prefix_entries(n: int, pieces: int, slots: int, width: int, stride: int) -> int:
     chunks = pieces * slots
     return 2 * n + pieces * stride + 2 * chunks + 1 + chunks * width
 
 
-def _prefix_view(flat: torch.Tensor, n: int, pieces: int, groups: int, width: int, *,
+def prefix_view(flat: torch.Tensor, n: int, pieces: int, groups: int, width: int, *,
                  members: int, max_members: int) -> PrefixGroups:  # fmt: skip
     chunks = pieces * groups
     at = [0]
@@ -247,7 +247,7 @@ def _prefix_view(flat: torch.Tensor, n: int, pieces: int, groups: int, width: in
                         pieces=pieces, max_members=max_members)  # fmt: skip
 
 
-def _fill_prefix(host: np.ndarray, n: int, pieces: int, slots: int, width: int,
+def fill_prefix(host: np.ndarray, n: int, pieces: int, slots: int, width: int,
                  tables: np.ndarray, groups: list[tuple[np.ndarray, int]], block_size: int,
                  stride: int) -> None:  # fmt: skip
     """Write ``groups`` into the flat layout above: ``slots`` chunks per piece, the

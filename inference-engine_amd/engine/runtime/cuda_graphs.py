@@ -70,7 +70,7 @@ class DecodeGraphs:
             for n in self.sizes:
                 k = pa.cascade_pieces(n, num_heads, nkv, dev)
                 self._shape[n] = (k, max_groups + 1, -(-w // k))
-                pre = max(pre, pa._prefix_entries(n, *self._shape[n], n))
+                pre = max(pre, pa.prefix_entries(n, *self._shape[n], n))
         self._pre_len = pre
         self._host = torch.zeros(3 * top + pre + top * w, dtype=torch.int32, pin_memory=True)
         self._meta = torch.zeros_like(self._host, device=dev)
@@ -115,7 +115,7 @@ class DecodeGraphs:
                            block_tables=self._tab[:n], context_lens=self._ctx[:n])  # fmt: skip
         if self.cascade:
             k, slots, width = self._shape[n]
-            batch.prefix_groups = pa._prefix_view(self._pre, n, k, slots, width, members=n,
+            batch.prefix_groups = pa.prefix_view(self._pre, n, k, slots, width, members=n,
                                                   max_members=n)  # fmt: skip
         return batch
 
@@ -149,7 +149,7 @@ class DecodeGraphs:
             # smallest ones to the plain decode
             groups.sort(key=lambda g: -len(g[0]) * g[1])
             groups = groups[: slots - 1]
-            pa._fill_prefix(self._h_pre, n, k, slots, width, self._h_tab, groups,
+            pa.fill_prefix(self._h_pre, n, k, slots, width, self._h_tab, groups,
                             self.cache.block_size, n)  # fmt: skip
             self.groups_last_step = len(groups)
 

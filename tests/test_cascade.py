@@ -162,13 +162,13 @@ def _static_layout(n, pieces, slots, width, tables, ctx, bs, min_blocks, groups=
     piece), filled on the host for one step's tables: (flat int32 array, groups used)."""
     import numpy as np
 
-    flat = np.zeros(pa._prefix_entries(n, pieces, slots, width, n), dtype=np.int32)
+    flat = np.zeros(pa.prefix_entries(n, pieces, slots, width, n), dtype=np.int32)
     tab = np.zeros((n, tables.shape[1]), dtype=np.int32)
     tab[: tables.shape[0]] = tables.numpy()
     if groups is None:
         groups = pa.shared_prefixes(tab[: tables.shape[0]], ctx.numpy(), bs, min_blocks)
     groups = groups[: slots - 1]
-    pa._fill_prefix(flat, n, pieces, slots, width, tab, groups, bs, n)
+    pa.fill_prefix(flat, n, pieces, slots, width, tab, groups, bs, n)
     return flat, groups
 
 
@@ -194,7 +194,7 @@ def test_static_prefix_layout_covers_every_context_exactly():
     width = -(-w // pieces)
     for min_blocks in (4, 10, 100):
         flat, groups = _static_layout(n, pieces, slots, width, tables, ctx, bs, min_blocks)
-        pg = pa._prefix_view(torch.from_numpy(flat), n, pieces, slots, width, members=n,
+        pg = pa.prefix_view(torch.from_numpy(flat), n, pieces, slots, width, members=n,
                              max_members=n)  # fmt: skip
         assert len(groups) == {4: 2, 10: 1, 100: 0}[min_blocks]
         cu = pg.cu_q.tolist()
@@ -246,13 +246,13 @@ def test_cascade_static_layout_graph_replays_match_oracle():
     nkv, bs, w = step.k_cache.shape[1], step.block_size, step.block_tables.shape[1]
     pieces = pa.cascade_pieces(n, nh, nkv, dev)
     slots, width = 3, -(-w // pieces)
-    meta = torch.zeros(pa._prefix_entries(n, pieces, slots, width, n), dtype=torch.int32,
+    meta = torch.zeros(pa.prefix_entries(n, pieces, slots, width, n), dtype=torch.int32,
                        device=dev)  # fmt: skip
     tables = torch.zeros(n, w, dtype=torch.int32, device=dev)
     ctx = torch.ones(n, dtype=torch.int32, device=dev)
     q = step.q.clone()
     out = torch.empty(n, nh, hd, dtype=torch.float32, device=dev)
-    pg = pa._prefix_view(meta, n, pieces, slots, width, members=n, max_members=n)
+    pg = pa.prefix_view(meta, n, pieces, slots, width, members=n, max_members=n)
 
     def call():
         pa.paged_decode_attention(q, step.k_cache, step.v_cache, tables, ctx, bs, out=out,
