@@ -51,7 +51,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "c2_1b"])
     ap.add_argument("--layers", type=int, default=4)
     ap.add_argument("--workgroups", type=int, default=None)
     ap.add_argument("--seed", type=int, default=0)
@@ -309,7 +309,7 @@ def bench_decode(args, torch) -> dict:
 def bench_cascade(args, torch, step, pools, out, wgs, unique_bytes) -> dict:
     """The same layer-steps with cascade decode as the engine's decode graphs run it:
     prefix groups found from the block tables on the host, laid out in the graphs'
-    fixed shape (2 group slots, pieces for the batch size), each shared prefix read once
+    fixed shape (one group slot, pieces for the batch size), each shared prefix read once
     per group; timed as hipGraph replays."""
     import numpy as np
 
@@ -321,7 +321,7 @@ def bench_cascade(args, torch, step, pools, out, wgs, unique_bytes) -> dict:
     groups = pa.shared_prefixes(tables, step.context_lens.cpu().numpy(), bs)
     if not groups:
         return {"cascade": None}
-    pieces, slots = pa.cascade_pieces(n, nh, nkv, step.q.device), 3
+    pieces, slots = pa.cascade_pieces(n, nh, nkv, step.q.device), 2  # DecodeGraphs' default
     width = -(-w // pieces)
     flat = np.zeros(pa.prefix_entries(n, pieces, slots, width, n), dtype=np.int32)
     groups.sort(key=lambda g: -len(g[0]) * g[1])

@@ -44,14 +44,16 @@ class DecodeGraphs:
     ``prefix_groups``: each shared prefix is read once per layer-step for its whole
     group. A step without groups runs the plain decode inside the same graph. Every
     chunk slot adds workgroups to the prefix pass whether a group fills it or not (at
-    config 3, 256 sequences: 129.6 us per layer-step with 1 slot for groups, 136.4 us
-    with 4), hence the default of 2 groups.
+    config 3, 256 sequences: 129.6 us per layer-step with 1 slot for groups, about 3 us
+    more per extra slot, 136.4 us with 4), hence the default of the one largest group
+    (one shared system prompt); engines with several popular prefixes raise
+    ``max_groups``.
     """
 
     def __init__(self, model: Callable, cache: PagedKVCache, scratch_block: int,
                  max_batch: int, max_blocks_per_seq: int, *, cascade: bool = False,
                  num_heads: int | None = None, cascade_min_blocks: int = 16,
-                 max_groups: int = 2) -> None:  # fmt: skip
+                 max_groups: int = 1) -> None:  # fmt: skip
         if max_batch < 1 or max_blocks_per_seq < 1:
             raise ValueError("DecodeGraphs: max_batch and max_blocks_per_seq must be >= 1")
         if cascade and not num_heads:

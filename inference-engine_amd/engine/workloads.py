@@ -135,6 +135,20 @@ def config2(device="cpu", seed: int = 0, batch: int = 64) -> DecodeStep:
                    device, gd)  # fmt: skip
 
 
+def config2_1b(device="cpu", seed: int = 0, batch: int = 64) -> DecodeStep:
+    """Config 2's batch and contexts (B=64, ctx ~ U[1024, 4096], bf16, block 16) at the
+    Llama-3.2-1B head shape of config 1 (32 q heads, 8 KV heads, hd 64): the head-dim-64
+    decode path at a bandwidth-bound size. Not a BASELINE config."""
+    g = torch.Generator().manual_seed(seed)
+    gd = _gen(device, seed + 1)
+    bs = 16
+    ctx = torch.randint(1024, 4097, (batch,), generator=g).tolist()
+    width = 4096 // bs
+    tables, nblk = _scattered(ctx, bs, 1.5, width, g)
+    return _finish("c2_llama1b_shape_bf16", ctx, tables, width, nblk, bs, 32, 8, 64,
+                   torch.bfloat16, device, gd)  # fmt: skip
+
+
 def config3(device="cpu", seed: int = 0, batch: int = 256, cow: int = 64) -> DecodeStep:
     """Prefix-shared decode at the 3B shape: every sequence's first 128 table entries are
     the same physical blocks (2,048 shared tokens), then a private tail of U[0, 1024]
@@ -279,4 +293,4 @@ def config5(device="cpu", seed: int = 0) -> MixedStep:
     )  # fmt: skip
 
 
-CONFIGS = {"c1": config1, "c2": config2, "c3": config3, "c4": config4}
+CONFIGS = {"c1": config1, "c2": config2, "c3": config3, "c4": config4, "c2_1b": config2_1b}
