@@ -321,11 +321,11 @@ def bench_cascade(args, torch, step, pools, out, wgs, unique_bytes) -> dict:
     groups = pa.shared_prefixes(tables, step.context_lens.cpu().numpy(), bs)
     if not groups:
         return {"cascade": None}
-    pieces, slots = pa.cascade_pieces(n, nh, nkv, step.q.device), 2  # DecodeGraphs' default
+    pieces, slots = pa.cascade_pieces(n, nh, nkv, step.q.device), 1  # DecodeGraphs' default
     width = -(-w // pieces)
     flat = np.zeros(pa.prefix_entries(n, pieces, slots, width, n), dtype=np.int32)
     groups.sort(key=lambda g: -len(g[0]) * g[1])
-    pa.fill_prefix(flat, n, pieces, slots, width, tables, groups[: slots - 1], bs, n)
+    pa.fill_prefix(flat, n, pieces, slots, width, tables, groups[:slots], bs, n)
     pg = pa.prefix_view(torch.from_numpy(flat).to(step.q.device), n, pieces, slots, width,
                         members=n, max_members=n)  # fmt: skip
 
@@ -338,8 +338,8 @@ def bench_cascade(args, torch, step, pools, out, wgs, unique_bytes) -> dict:
     gbps = unique_bytes / (us * 1e-6) / 1e9
     return {"cascade_us": round(us, 2), "cascade_unique_gbps": round(gbps, 1),
             "cascade_unique_frac": round(gbps / HBM_PEAK_GBPS, 4),
-            "cascade_groups": min(len(groups), slots - 1), "cascade_pieces": pieces,
-            "cascade_layout": f"decode-graph fixed shape: {slots - 1} group slots"}
+            "cascade_groups": min(len(groups), slots), "cascade_pieces": pieces,
+            "cascade_layout": f"decode-graph fixed shape: {slots} group slot(s)"}
 
 
 def bench_cow(torch, step, layers: int = 28, blocks: int = 2048) -> dict:

@@ -67,9 +67,10 @@ struct DecodeArgs {
   // Cascade (pre_row non-null): normalised attentions of the same queries over other
   // keys (a shared prefix's pieces), merged into the result by the combine pass. Part k
   // of sequence b is row pre_row[b] + k * pre_stride of pre_o [rows, nh, HD] / pre_lse
-  // [rows, nh] (pre_row[b] < 0: none). The stream pass then writes the sequences it
-  // finishes to out / lse as fp32 scratch, and the combine pass writes every sequence's
-  // result to fin (fin_f32: fp32, else DT) and its normaliser to fin_lse (if non-null).
+  // [rows, nh] (pre_row[b] < 0: none). The stream pass then writes the sequences with
+  // parts it finishes to out / lse as fp32 scratch, and the combine pass writes every
+  // other sequence's result to fin (fin_f32: fp32, else DT) and its normaliser to
+  // fin_lse (if non-null); a whole sequence without parts the stream pass writes there.
   const float* pre_o;
   const float* pre_lse;
   const int32_t* pre_row;
@@ -86,6 +87,20 @@ __device__ __forceinline__ int first_blk(const DecodeArgs& a, int b) {
   if (!a.first_block) return 0;
   const int f = a.first_block[b];
   return f < 0 ? 0 : (f > a.max_blocks ? a.max_blocks : f);
+}
+
+// Where the stream pass writes a sequence it finishes whole: the result (out), except
+// in cascade for a sequence with prefix parts (pre_b >= 0), whose fp32 state goes to
+// scratch (out, lse at that point) for the combine to merge; without parts it is final.
+struct WholeDst {
+  void* p;
+  int64_t sb, sh;
+  bool f32;
+  float* lse;
+};
+__device__ __forceinline__ WholeDst whole_dst(const DecodeArgs& a, int pre_b) {
+  if (a.pre_row && pre_b < 0) return {a.fin, a.fin_sb, a.fin_sh, a.fin_f32 != 0, a.fin_lse};
+  return {a.out, a.out_sb, a.out_sh, a.out_f32 != 0, a.lse};
 }
 
 // Tokens sequence b attends to, clamped: 0 <= n <= (max_blocks - first) * block_size.
@@ -284,6 +299,7 @@ paged_decode_stream_kernel(const DecodeArgs a) {
     // Block ids of up to 64 consecutive blocks starting at cb, one per lane.
     int cb = 0, tbl = 0;
     const int fb = first_blk(a, b);
+    const int pre_b = a.pre_row ? a.pre_row[b] : -1;  // cascade: b's prefix row, or none
     auto load_table = [&](int first_block) {
       cb = first_block;
       const int j = cb + lane;
@@ -401,6 +417,7 @@ paged_decode_stream_kernel(const DecodeArgs a) {
 
     if (lane < LPT) {
       if (whole) {  // the whole context was in this range: final output directly
+        const WholeDst dst = whole_dst(a, pre_b);
 #pragma unroll
         for (int g = 0; g < GPW; ++g) {
           // no live token (empty context): 0, the reference oracle's einsum over no keys
@@ -408,10 +425,10 @@ paged_decode_stream_kernel(const DecodeArgs a) {
           float o[VEC];
 #pragma unroll
           for (int c = 0; c < VEC; ++c) o[c] = acc[g][c] * inv;
-          const int64_t e = b * a.out_sb + (int64_t)(h0 + g) * a.out_sh + d0;
-          if (a.out_f32) store_vec<PKV_F32, VEC>((float*)a.out + e, o);
-          else store_vec<DT, VEC>((S*)a.out + e, o);
-          if (a.lse && lane == 0) a.lse[(int64_t)b * a.nh + h0 + g] = lse_of(m[g], l[g]);
+          const int64_t e = b * dst.sb + (int64_t)(h0 + g) * dst.sh + d0;
+          if (dst.f32) store_vec<PKV_F32, VEC>((float*)dst.p + e, o);
+          else store_vec<DT, VEC>((S*)dst.p + e, o);
+          if (dst.lse && lane == 0) dst.lse[(int64_t)b * a.nh + h0 + g] = lse_of(m[g], l[g]);
         }
       } else {
 #pragma unroll
@@ -647,6 +664,7 @@ paged_decode_mfma_kernel(const DecodeArgs a) {
 
     int cb = 0, tbl = 0;
     const int fb = first_blk(a, b);
+    const int pre_b = a.pre_row ? a.pre_row[b] : -1;  // cascade: b's prefix row, or none
     auto load_table = [&](int first_block) {
       cb = first_block;
       const int j = cb + lane;
@@ -960,16 +978,17 @@ paged_decode_mfma_kernel(const DecodeArgs a) {
     if (grp == 0 && col < VC) {  // lane c writes head dims 8c .. 8c + 7
       const int d0 = 8 * col;
       if (whole) {
+        const WholeDst dst = whole_dst(a, pre_b);
 #pragma unroll
         for (int g = 0; g < GPW; ++g) {
           const float inv = lh[g] > 0.f ? 1.f / lh[g] : 0.f;
           float o[8];
 #pragma unroll
           for (int d = 0; d < 8; ++d) o[d] = acc[g][d] * inv;
-          const int64_t e = b * a.out_sb + (int64_t)(h0 + g) * a.out_sh + d0;
-          if (a.out_f32) store_vec<PKV_F32, 8>((float*)a.out + e, o);
-          else store_vec<DT, 8>((S*)a.out + e, o);
-          if (a.lse && col == 0) a.lse[(int64_t)b * a.nh + h0 + g] = lse_of(mh[g], lh[g]);
+          const int64_t e = b * dst.sb + (int64_t)(h0 + g) * dst.sh + d0;
+          if (dst.f32) store_vec<PKV_F32, 8>((float*)dst.p + e, o);
+          else store_vec<DT, 8>((S*)dst.p + e, o);
+          if (dst.lse && col == 0) dst.lse[(int64_t)b * a.nh + h0 + g] = lse_of(mh[g], lh[g]);
         }
       } else {
 #pragma unroll
@@ -1046,10 +1065,12 @@ paged_decode_combine_kernel(const DecodeArgs a) {
 
   const int4 plan = a.desc[b];
   const bool cascade = a.pre_row != nullptr;
-  const int pre = cascade && part == 0 ? a.pre_row[b] : -1;  // fetched with the plan
+  const int pre_b = cascade ? a.pre_row[b] : -1;  // fetched with the plan
+  const int pre = part == 0 ? pre_b : -1;
   const int nrec = plan.y;
-  // Written directly by the stream pass (or past the batch): nothing to merge.
-  const bool skip = !active || (nrec <= 1 && !cascade);
+  // Written directly by the stream pass (or past the batch): nothing to merge -- in
+  // cascade, a whole sequence without prefix parts.
+  const bool skip = !active || (nrec <= 1 && pre_b < 0);
   if (SP == 1 && skip) return;
   // This wave's records [jb, je): all of them, or one half of them.
   const int jb = part == 0 ? 0 : (nrec + 1) / 2;

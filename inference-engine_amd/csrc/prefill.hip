@@ -273,6 +273,14 @@ paged_prefill_kernel(const PrefillArgs a) {
 #pragma unroll
     for (int s = 0; s < KS; ++s) qf[t][s] = *reinterpret_cast<const u32x4*>(qp + 32 * s);
   }
+  // A row block of padding only (every q_rows entry negative: a fixed-shape layout's
+  // spare rows) leaves before any key tile; the test is workgroup-uniform.
+  if (a.q_rows) {
+    bool any = false;
+#pragma unroll
+    for (int t = 0; t < RT; ++t) any = any || row_ok[t];
+    if (!__syncthreads_or(any)) return;
+  }
   // Keys any row of this workgroup attends to: [0, kend), in ntiles tiles; half 0 takes
   // tiles 0 .. ns - 1, half 1 the other ntiles - ns.
   const int last_row = min(nrows - 1, rho0 + BM - 1);

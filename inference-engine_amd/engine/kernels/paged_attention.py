@@ -248,16 +248,15 @@ def prefix_view(flat: torch.Tensor, n: int, pieces: int, groups: int, width: int
 
 
 def fill_prefix(host: np.ndarray, n: int, pieces: int, slots: int, width: int,
-                 tables: np.ndarray, groups: list[tuple[np.ndarray, int]], block_size: int,
-                 stride: int) -> None:  # fmt: skip
-    """Write ``groups`` into the flat layout above: ``slots`` chunks per piece, the
-    groups' member rows ``stride`` apart between pieces. Sequences outside every group
-    get first_block 0 and prefix_row -1. Rows of a piece past its groups' members (when
-    stride exceeds them) belong to the piece's last chunk, which then must be free of
-    groups; their q_rows entry is -1, so the prefix pass skips them."""
-    used = groups[: slots - 1] if stride > sum(len(m) for m, _ in groups) else groups
-    if len(used) > slots:
-        raise ValueError(f"prefix groups: {len(used)} groups for {slots} chunk slots")
+                tables: np.ndarray, groups: list[tuple[np.ndarray, int]], block_size: int,
+                stride: int) -> None:  # fmt: skip
+    """Write ``groups`` (at most ``slots``) into the flat layout above: ``slots`` chunks per
+    piece, the groups' member rows ``stride`` apart between pieces. Sequences outside
+    every group get first_block 0 and prefix_row -1. Rows of a piece past its groups'
+    members (when stride exceeds them) belong to the piece's last chunk, with q_rows -1:
+    the prefix pass skips them (a workgroup holding only such rows leaves at once)."""
+    if len(groups) > slots:
+        raise ValueError(f"prefix groups: {len(groups)} groups for {slots} chunk slots")
     chunks = pieces * slots
     o_pr, o_qr = n, 2 * n
     o_cu = o_qr + pieces * stride
@@ -268,7 +267,7 @@ def fill_prefix(host: np.ndarray, n: int, pieces: int, slots: int, width: int,
     host[o_qr : o_qr + pieces * stride] = -1
     ptab = host[o_tab : o_tab + chunks * width].reshape(chunks, width)
     ends, row = [], 0
-    for g, (members, shared) in enumerate(used):
+    for g, (members, shared) in enumerate(groups):
         size = len(members)
         host[members] = shared  # first_block
         host[o_pr + members] = np.arange(row, row + size)
@@ -281,8 +280,10 @@ def fill_prefix(host: np.ndarray, n: int, pieces: int, slots: int, width: int,
             host[o_ctx + c] = (hi - lo) * block_size
         row += size
         ends.append(row)
-    # cu_q: chunk k * slots + g ends at k S + (its group's last row); the free chunks of
-    # a piece are empty but for the last, which runs to the next piece's first row.
+    if row > stride:
+        raise ValueError(f"prefix groups: {row} member rows for a stride of {stride}")
+    # cu_q: chunk k * slots + g ends at k S + (its group's last row); unused chunks of a
+    # piece are empty but for the last, which runs to the next piece's first row.
     cu = np.zeros(chunks + 1, dtype=np.int64)
     for k in range(pieces):
         for g in range(slots):

@@ -39,15 +39,14 @@ class DecodeGraphs:
     ``cascade`` (needs the model's ``num_heads``): every step also looks for sequences
     whose tables start with the same blocks (``shared_prefixes``, at least
     ``cascade_min_blocks``; the ``max_groups`` largest groups) and lays them out in the
-    prefix-groups region in a fixed shape per bucket -- K pieces, max_groups + 1 chunks
-    per piece, member rows n apart -- which the captured decode calls read as their
+    prefix-groups region in a fixed shape per bucket -- K pieces, max_groups chunks per
+    piece, member rows n apart -- which the captured decode calls read as their
     ``prefix_groups``: each shared prefix is read once per layer-step for its whole
     group. A step without groups runs the plain decode inside the same graph. Every
     chunk slot adds workgroups to the prefix pass whether a group fills it or not (at
-    config 3, 256 sequences: 129.6 us per layer-step with 1 slot for groups, about 3 us
-    more per extra slot, 136.4 us with 4), hence the default of the one largest group
-    (one shared system prompt); engines with several popular prefixes raise
-    ``max_groups``.
+    config 3, 256 sequences: 128.7 us per layer-step with one slot, 129.5 with two),
+    hence the default of the one largest group (one shared system prompt); engines with
+    several popular prefixes raise ``max_groups``.
     """
 
     def __init__(self, model: Callable, cache: PagedKVCache, scratch_block: int,
@@ -71,7 +70,7 @@ class DecodeGraphs:
             nkv = cache.k.shape[2]
             for n in self.sizes:
                 k = pa.cascade_pieces(n, num_heads, nkv, dev)
-                self._shape[n] = (k, max_groups + 1, -(-w // k))
+                self._shape[n] = (k, max_groups, -(-w // k))
                 pre = max(pre, pa.prefix_entries(n, *self._shape[n], n))
         self._pre_len = pre
         self._host = torch.zeros(3 * top + pre + top * w, dtype=torch.int32, pin_memory=True)
@@ -150,7 +149,7 @@ class DecodeGraphs:
             # the largest first: a step with more groups than chunk slots leaves the
             # smallest ones to the plain decode
             groups.sort(key=lambda g: -len(g[0]) * g[1])
-            groups = groups[: slots - 1]
+            groups = groups[:slots]
             pa.fill_prefix(self._h_pre, n, k, slots, width, self._h_tab, groups,
                             self.cache.block_size, n)  # fmt: skip
             self.groups_last_step = len(groups)

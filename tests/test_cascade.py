@@ -167,17 +167,17 @@ def _static_layout(n, pieces, slots, width, tables, ctx, bs, min_blocks, groups=
     tab[: tables.shape[0]] = tables.numpy()
     if groups is None:
         groups = pa.shared_prefixes(tab[: tables.shape[0]], ctx.numpy(), bs, min_blocks)
-    groups = groups[: slots - 1]
+    groups = groups[:slots]
     pa.fill_prefix(flat, n, pieces, slots, width, tab, groups, bs, n)
     return flat, groups
 
 
 def test_static_prefix_layout_covers_every_context_exactly():
-    """The fixed layout of a graph bucket (n rows apart between pieces, one more chunk
-    slot per piece than groups): every grouped sequence's prefix pieces plus its tail
-    visit exactly its own slots; rows past the groups' members sit in the piece's last
-    chunk, have no keys and q_rows -1; padding rows and ungrouped sequences get no
-    prefix; cu_q never decreases and ends at pieces * n."""
+    """The fixed layout of a graph bucket (n rows apart between pieces, a fixed number of
+    chunk slots per piece): every grouped sequence's prefix pieces plus its tail visit
+    exactly its own slots; rows past the groups' members sit in the piece's last chunk
+    with q_rows -1 (whether or not a group holds that chunk); padding rows and
+    ungrouped sequences get no prefix; cu_q never decreases and ends at pieces * n."""
     import numpy as np
 
     bs = 16
@@ -190,21 +190,21 @@ def test_static_prefix_layout_covers_every_context_exactly():
     tables[:10, : t1.shape[1]] = t1
     tables[10:16, : t2.shape[1]] = t2
     ctx = torch.cat([c1, c2])
-    n, pieces, slots = 24, 3, 4  # bucket 24 for 16 sequences
+    n, pieces = 24, 3  # bucket 24 for 16 sequences
     width = -(-w // pieces)
-    for min_blocks in (4, 10, 100):
+    for min_blocks, slots in ((4, 4), (4, 2), (4, 1), (10, 1), (100, 1)):
         flat, groups = _static_layout(n, pieces, slots, width, tables, ctx, bs, min_blocks)
         pg = pa.prefix_view(torch.from_numpy(flat), n, pieces, slots, width, members=n,
                              max_members=n)  # fmt: skip
-        assert len(groups) == {4: 2, 10: 1, 100: 0}[min_blocks]
+        assert len(groups) == min({4: 2, 10: 1, 100: 0}[min_blocks], slots)
         cu = pg.cu_q.tolist()
         assert cu[0] == 0 and cu[-1] == pieces * n and all(a <= b for a, b in zip(cu, cu[1:]))
         chunk_of = np.searchsorted(np.asarray(cu), np.arange(pieces * n), side="right") - 1
         members = sum(len(m) for m, _ in groups)
         for k in range(pieces):
-            for r in range(members, n):  # rows past the members: skipped, no keys
+            for r in range(members, n):  # rows past the members: skipped
                 row = k * n + r
-                assert int(pg.q_rows[row]) == -1 and int(pg.ctx[chunk_of[row]]) == 0
+                assert int(pg.q_rows[row]) == -1 and chunk_of[row] == k * slots + slots - 1
         for b in range(n):
             r = int(pg.prefix_row[b])
             fb = int(pg.first_block[b])
@@ -222,7 +222,7 @@ def test_static_prefix_layout_covers_every_context_exactly():
                     seen += [int(pg.tables[c, p // bs]) * bs + p % bs for p in range(int(pg.ctx[c]))]
             assert (r >= 0) == (fb > 0)
             seen += [int(tables[b, fb + p // bs]) * bs + p % bs for p in range(seqn - fb * bs)]
-            assert seen == own, (min_blocks, b)
+            assert seen == own, (min_blocks, slots, b)
 
 
 @pytest.mark.gpu
@@ -245,7 +245,7 @@ def test_cascade_static_layout_graph_replays_match_oracle():
     n, nh, hd = step.q.shape
     nkv, bs, w = step.k_cache.shape[1], step.block_size, step.block_tables.shape[1]
     pieces = pa.cascade_pieces(n, nh, nkv, dev)
-    slots, width = 3, -(-w // pieces)
+    slots, width = 2, -(-w // pieces)  # two groups fill both: spare rows join the second's
     meta = torch.zeros(pa.prefix_entries(n, pieces, slots, width, n), dtype=torch.int32,
                        device=dev)  # fmt: skip
     tables = torch.zeros(n, w, dtype=torch.int32, device=dev)
