@@ -308,3 +308,46 @@ def test_cascade_static_layout_graph_replays_match_oracle():
         err = (out[:b].cpu() - want).abs().max().item()
         assert err <= 2e-3, (name, err)
         assert np.isfinite(out.cpu().numpy()).all(), name
+
+
+def test_prefix_groups_must_match_the_call():
+    """A PrefixGroups built for another step is refused before any launch: the kernels
+    read first_block[b] and prefix_row[b] for every sequence b and the prefix pass's
+    tables by chunk, so wrong lengths, dtypes or layouts would read out of bounds."""
+    import dataclasses
+
+    tables, ctx, _ = _shared_batch(seed=3)
+    pg = pa.find_prefix_groups(tables, ctx, 16, 24, 8, "cpu", min_blocks=4,
+                               target_workgroups=64)  # fmt: skip
+    cpu = torch.device("cpu")
+    b = tables.shape[0]
+    pa._check_prefix_groups(pg, b, cpu, "t")  # the step it was built for
+    with pytest.raises(ValueError, match="built for"):
+        pa._check_prefix_groups(pg, b + 1, cpu, "t")
+    for name in ("first_block", "prefix_row", "q_rows", "cu_q", "ctx", "tables"):
+        t = getattr(pg, name)
+        for bad in (t.long(), t.t() if t.dim() == 2 else t[::2]):
+            if bad.dtype == torch.int32 and bad.is_contiguous() and bad.shape == t.shape:
+                continue
+            with pytest.raises(ValueError):
+                pa._check_prefix_groups(dataclasses.replace(pg, **{name: bad}), b, cpu, "t")
+    with pytest.raises(ValueError, match="disagree"):
+        pa._check_prefix_groups(dataclasses.replace(pg, pieces=pg.pieces + 1), b, cpu, "t")
+    with pytest.raises(ValueError, match="disagree"):
+        pa._check_prefix_groups(dataclasses.replace(pg, cu_q=pg.cu_q[:-1].contiguous()), b,
+                                cpu, "t")  # fmt: skip
+
+
+@pytest.mark.gpu
+def test_decode_refuses_prefix_groups_of_another_step():
+    """Through paged_decode_attention on the GPU: groups built for a 12-sequence step,
+    called with 11 sequences, raise ValueError and launch nothing."""
+    dev = torch.device("cuda:0")
+    tables, ctx, nblk = _shared_batch(seed=8)
+    k = torch.randn(nblk * 16, 8, 128, device=dev).to(torch.bfloat16)
+    q = torch.randn(tables.shape[0], 24, 128, device=dev).to(torch.bfloat16)
+    pg = pa.find_prefix_groups(tables, ctx, 16, 24, 8, dev, min_blocks=4)
+    assert pg is not None
+    with pytest.raises(ValueError, match="built for"):
+        pa.paged_decode_attention(q[:-1], k, k, tables[:-1].to(dev), ctx[:-1].to(dev), 16,
+                                  prefix_groups=pg)  # fmt: skip
