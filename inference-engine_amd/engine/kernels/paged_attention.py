@@ -1,23 +1,29 @@
-"""Paged decode attention on MI355X (gfx950), same call signatures as the reference's
+"""Paged attention on MI355X (gfx950), same call signatures as the reference's
 ``engine/kernels/paged_attention.py``.
 
-``paged_decode_attention`` runs two hand-written HIP kernels through the C ABI of
-lib/libpaged_kv.so:
+``paged_decode_attention`` runs hand-written HIP kernels through the C ABI of
+lib/libpaged_kv.so, chosen by the library from static shapes:
 
 1. a stream-K pass: the contexts of all sequences, laid end to end, are split evenly
    over as many workgroups as the GPU holds at once. One wave per KV head streams its
    share of K/V rows straight from the paged pool through the block table with 16-byte
    non-temporal loads, computes the scores of every query head sharing that KV head
    (GQA: each K/V row is read once for the whole group; on the matrix cores for 16-bit
-   caches at head_dim 128) and keeps an fp32 online softmax. Sequences inside one
-   workgroup's share are written directly.
-2. a combine pass that merges, with log-sum-exp weights, the pieces of the sequences
-   cut by a share boundary.
+   caches at head_dim 64 and 128) and keeps an fp32 online softmax. Sequences inside one
+   workgroup's share are written directly; a combine pass merges, with log-sum-exp
+   weights, the pieces of the sequences cut by a share boundary.
+2. for small batches (every sequence's KV heads fit the CUs), one launch in which a
+   workgroup's waves split one sequence and merge through LDS: no combine, no scratch.
 
-The grid depends only on the device and static shapes, never on the context lengths
+With ``prefix_groups`` (cascade decode) the shared prefix of each group is attended once
+for all its members by the chunked-prefill kernel (``paged_prefill_attention``'s), and
+the decode passes read only each sequence's private blocks.
+
+The grids depend only on the device and static shapes, never on the context lengths
 (device data), so one hipGraph capture serves every length, as the reference's
 CUDA-graph decode requires (reference engine/runtime/cuda_graphs.py:10-11). Nothing here
-allocates outside torch's caching allocator or synchronises.
+allocates outside torch's caching allocator or synchronises (the opt-in metadata checks
+of ``_native.set_debug_checks`` excepted).
 """
 
 from __future__ import annotations
