@@ -283,6 +283,11 @@ def bench_decode(args, torch) -> dict:
             "traffic": traffic,
         },
         "traffic_source": traffic_source,
+        # achieved / frac cover the whole decode call the C ABI exposes (one
+        # pkv_paged_decode: the split pass, or the stream pass + combine); traffic is the
+        # stream pass's (the combine's own bytes are in the profile summary)
+        "roofline_scope": "pkv_paged_decode call (" +
+                          ("split pass" if plan == 0 else "stream pass + combine") + ")",
         "kv_bytes_per_step": kv_bytes,
         "eager_us": round(eager_mean, 2),
         "eager_median_us": round(statistics.median(per), 2),

@@ -248,6 +248,35 @@ def test_engine_cascade_decode_matches_plain(dtype):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("groups", [1, 2])
+def test_decode_graphs_cascade_two_prefix_families(groups):
+    """Two prompt families, each sharing its own prefix: with one group slot the graphs
+    cascade the larger family and decode the other plainly, with two both -- the plain
+    decode's tokens either way."""
+    from tiny_llama import KernelBackend
+
+    model = _cuda_model(torch.bfloat16)
+    other = [40, 41, 42, 43, 44, 45, 46, 47, 48, 49, 50, 51]
+    prompts = {"b": SHARED + [1, 2], "d": SHARED + [3], "f": SHARED, "p": other + [9],
+               "q": other, "r": other + [7, 8]}  # fmt: skip
+    runs = {}
+    for graphs, min_blocks in ((False, None), (True, 2)):
+        eng = TinyEngine(model, KernelBackend(), num_blocks=96, block_size=4, max_num_seqs=8,
+                         graphs=graphs, cascade_min_blocks=min_blocks,
+                         cascade_groups=groups)  # fmt: skip
+        runs[graphs] = (_run_staggered(eng, prompts, 10), eng)
+    log = runs[True][1].log
+    assert any(s["graph"] and s["cascade"] for s in log)
+    assert max(s["groups"] for s in log if s["graph"]) == groups
+    assert runs[True][0] == runs[False][0]
+    worst = max((torch.stack(runs[True][1].logits[r]) -
+                 torch.stack(runs[False][1].logits[r])).abs().max().item()
+                for r in prompts)  # fmt: skip
+    assert worst <= 0.05, worst
+    assert runs[True][1].bm.num_free_blocks == 96
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_decode_graphs_cascade_matches_plain(dtype):
     """Decode steps replayed from hipGraphs with cascade on: each step's prefix groups

@@ -290,7 +290,7 @@ class TinyEngine:
                  max_num_seqs: int = 8, max_num_batched_tokens: int = 4096,
                  share_prefixes: bool = True, graphs: bool = False,
                  mixed_graphs: bool = False, debug_checks: bool = True,
-                 cascade_min_blocks: int | None = None) -> None:  # fmt: skip
+                 cascade_min_blocks: int | None = None, cascade_groups: int = 1) -> None:  # fmt: skip
         self.model, self.backend = model, backend
         w = model.embed.weight
         self.device, self.dtype = w.device, w.dtype
@@ -318,7 +318,7 @@ class TinyEngine:
             self.graphs = DecodeGraphs(
                 model, self.cache, num_blocks, max_num_seqs, num_blocks,
                 cascade=cascade_min_blocks is not None, num_heads=cfg.num_attention_heads,
-                cascade_min_blocks=cascade_min_blocks or 16)  # fmt: skip
+                cascade_min_blocks=cascade_min_blocks or 16, max_groups=cascade_groups)  # fmt: skip
         self.mixed_graphs = None
         if mixed_graphs:
             from engine.runtime.cuda_graphs import MixedGraphs
@@ -447,9 +447,12 @@ class TinyEngine:
             cascaded = self.graphs.groups_last_step > 0
         else:
             cascaded = not used_mixed_graph and batch.prefix_groups is not None
+        groups = self.graphs.groups_last_step if used_graph else (
+            batch.prefix_groups.ctx.numel() // batch.prefix_groups.pieces
+            if cascaded else 0)  # fmt: skip
         self.log.append({"seqs": len(plan), "tokens": len(ids), "decode_only": decode_only,
                          "graph": used_graph, "mixed_graph": used_mixed_graph,
-                         "copies": len(pairs), "cascade": cascaded})  # fmt: skip
+                         "copies": len(pairs), "cascade": cascaded, "groups": groups})  # fmt: skip
         return outputs
 
     def generate(self, prompts: dict[str, list[int]], max_tokens: int) -> dict[str, list[int]]:
