@@ -249,6 +249,62 @@ __device__ __forceinline__ void write_desc(const DecodeArgs& a, int b, int w, in
   a.desc[b] = make_int4(w, (int)(w1 - w + 1), rs < ub ? 1 : 0, total >= a.num_wg ? 1 : 0);
 }
 
+// Batches of kWave + 1 .. kLdsBatch sequences: every sequence's clamped context, first
+// table column, cascade prefix row and first unit, staged in LDS by the whole workgroup.
+// All lengths arrive in one memory trip (find_unit takes one dependent trip per 64
+// sequences, twice), the range's first sequence is a binary search in LDS, and a
+// sequence boundary inside a range needs no trip for the next sequence's length.
+constexpr int kLdsBatch = 1024;
+struct BatchLds {
+  int64_t ub[kLdsBatch + 1];  // first unit of each sequence; ub[batch] = total units
+  int n[kLdsBatch], fb[kLdsBatch], pre[kLdsBatch];
+  int64_t wsum[PKV_DECODE_WAVES_PER_WG];  // per-wave unit sums of the scan
+};
+// Fill s (whole workgroup; blockDim.x <= 64 * PKV_DECODE_WAVES_PER_WG). Thread t takes a
+// contiguous run of sequences, so one wave scan plus the waves' totals give every prefix.
+__device__ void stage_batch(const DecodeArgs& a, BatchLds& s) {
+  const int tid = threadIdx.x, nt = blockDim.x;
+  const int lane = tid & (kWave - 1), wave = tid / kWave;
+  const int per = (a.batch + nt - 1) / nt;
+  const int b0 = tid * per, b1 = min(a.batch, b0 + per);
+  int64_t mine = 0;
+  for (int b = b0; b < b1; ++b) {
+    const int fb = first_blk(a, b);
+    const int n = clamped_ctx(a, b);
+    s.n[b] = n;
+    s.fb[b] = fb;
+    s.pre[b] = a.pre_row ? a.pre_row[b] : -1;
+    mine += units_of(a, n);
+  }
+  int64_t incl = mine;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int64_t t = __shfl_up(incl, off);
+    if (lane >= off) incl += t;
+  }
+  if (lane == kWave - 1) s.wsum[wave] = incl;
+  __syncthreads();
+  int64_t before = incl - mine;
+  for (int w = 0; w < wave; ++w) before += s.wsum[w];
+  for (int b = b0; b < b1; ++b) {
+    s.ub[b] = before;
+    before += units_of(a, s.n[b]);
+  }
+  if (tid == nt - 1) s.ub[a.batch] = before;  // the last thread's run ends the batch
+  __syncthreads();
+}
+// The sequence owning unit u < total: the last b with ub[b] <= u (every sequence owns at
+// least one unit, so ub is strictly increasing).
+__device__ __forceinline__ int staged_owner(const DecodeArgs& a, const BatchLds& s, int64_t u) {
+  int lo = 0, hi = a.batch - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (s.ub[mid] <= u) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
+}
+
 template <int DT, int HD, int GPW>
 __global__ void __launch_bounds__(512)
 paged_decode_stream_kernel(const DecodeArgs a) {
@@ -565,7 +621,7 @@ __device__ __forceinline__ void split_merge(const DecodeArgs& a, int b, int h0,
   }
 }
 
-template <int DT, int GPW, bool FAST, int HD, bool SPLIT>
+template <int DT, int GPW, bool FAST, int HD, bool SPLIT, bool STAGED = false>
 __global__ void __launch_bounds__(512)
 paged_decode_mfma_kernel(const DecodeArgs a) {
   // hd 128: a step is one 16-token tile, four 32-dim MFMA k-blocks, V rows over all 16
@@ -585,7 +641,7 @@ paged_decode_mfma_kernel(const DecodeArgs a) {
   const int task = SPLIT ? (int)blockIdx.y
                          : (int)(blockIdx.y * (blockDim.x / kWave) + (threadIdx.x / kWave));
   const int kvh = task / a.nsub;
-  if (!SPLIT && kvh >= a.nkv) return;
+  if (!SPLIT && !STAGED && kvh >= a.nkv) return;
   const int h0 = kvh * a.groups + (task - kvh * a.nsub) * GPW;
   const int w = blockIdx.x;
 
@@ -595,6 +651,11 @@ paged_decode_mfma_kernel(const DecodeArgs a) {
   // the same memory trip as each wave's context length (the split's tables hold at most
   // kSplitMaxColumns entries), so no wave waits for its length before its block ids.
   __shared__ int split_table[SPLIT ? kSplitMaxColumns : 1];
+  // STAGED (stream-K over kWave + 1 .. kLdsBatch sequences): the batch's metadata in LDS.
+  // Smaller batches keep their lengths in lanes; larger ones walk them with find_unit.
+  static_assert(!(SPLIT && STAGED), "the split pass takes one sequence per workgroup");
+  __shared__ BatchLds batch_lds[1];  // unused (and dropped) unless STAGED
+  constexpr bool staged = STAGED;
   int split_n = 0;
   if constexpr (SPLIT) {
     total = rs = ub = 0;
@@ -604,9 +665,17 @@ paged_decode_mfma_kernel(const DecodeArgs a) {
     for (int j = threadIdx.x; j < a.max_blocks; j += blockDim.x)
       split_table[j] = a.tables[(int64_t)b * a.table_stride + j];
     __syncthreads();
+  } else if constexpr (STAGED) {  // every wave of the workgroup stages, then idle ones leave
+    stage_batch(a, batch_lds[0]);
+    total = batch_lds[0].ub[a.batch];
+    rs = range_start(w, total, a.num_wg);
+    re = range_start(w + 1, total, a.num_wg);
+    b = rs < re ? staged_owner(a, batch_lds[0], rs) : a.batch;
+    ub = rs < re ? batch_lds[0].ub[b] : 0;
   } else {
     b = locate_range(a, w, &total, &rs, &re, &ub);
   }
+  if (STAGED && kvh >= a.nkv) return;
   if (rs >= re) return;
 
   const int col = lane & 15, grp = lane >> 4;
@@ -622,7 +691,7 @@ paged_decode_mfma_kernel(const DecodeArgs a) {
   for (int64_t u = rs; u < re && b < a.batch; ++b) {
     int n;
     if constexpr (SPLIT) n = split_n;
-    else n = clamped_ctx(a, b);
+    else n = staged ? batch_lds[0].n[b] : clamped_ctx(a, b);
     int t0, t1, slot = 0;
     bool whole = true;
     if constexpr (SPLIT) {  // this wave's 16-token-aligned share of the context
@@ -663,8 +732,9 @@ paged_decode_mfma_kernel(const DecodeArgs a) {
     }
 
     int cb = 0, tbl = 0;
-    const int fb = first_blk(a, b);
-    const int pre_b = a.pre_row ? a.pre_row[b] : -1;  // cascade: b's prefix row, or none
+    const int fb = staged ? batch_lds[0].fb[b] : first_blk(a, b);
+    // cascade: b's prefix row, or none
+    const int pre_b = staged ? batch_lds[0].pre[b] : (a.pre_row ? a.pre_row[b] : -1);
     auto load_table = [&](int first_block) {
       cb = first_block;
       const int j = cb + lane;
@@ -1296,8 +1366,13 @@ struct LaunchDecode {
   template <int DT, int HD, int GPW> hipError_t run() const {
     const dim3 grid((unsigned)a->num_wg, (unsigned)ygrid), block(kWave * wpg);
     if constexpr (use_mfma<DT, HD>()) {
-      if (a->bs % 16 == 0)
+      const bool staged = a->batch > kWave && a->batch <= kLdsBatch;
+      if (a->bs % 16 == 0 && staged)
+        hipLaunchKernelGGL((paged_decode_mfma_kernel<DT, GPW, true, HD, false, true>), grid, block, 0, st, *a);
+      else if (a->bs % 16 == 0)
         hipLaunchKernelGGL((paged_decode_mfma_kernel<DT, GPW, true, HD, false>), grid, block, 0, st, *a);
+      else if (staged)
+        hipLaunchKernelGGL((paged_decode_mfma_kernel<DT, GPW, false, HD, false, true>), grid, block, 0, st, *a);
       else
         hipLaunchKernelGGL((paged_decode_mfma_kernel<DT, GPW, false, HD, false>), grid, block, 0, st, *a);
     } else {

@@ -52,6 +52,34 @@ def test_decode_random_shape(seed):
     assert torch.equal(outq.cpu(), out32.cpu().to(dtype))
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_decode_random_large_batch(seed):
+    """Batches past one wave (65 .. 1,100 sequences): the stream pass stages the batch's
+    lengths, first columns and unit offsets in LDS up to 1,024 sequences and walks them
+    64 at a time beyond that; ragged and empty contexts, work splits that leave ranges
+    empty or cut every sequence."""
+    r = random.Random(500 + seed)
+    hd = r.choice([64, 128, 128])
+    nkv = r.choice([1, 2, 8])
+    groups = r.choice([1, 3, 4])
+    bs = r.choice([8, 12, 16, 16, 32])
+    dtype = r.choice([torch.bfloat16, torch.float16])
+    batch = r.choice([65, r.randint(66, 300), r.randint(300, 1024), r.randint(1025, 1100)])
+    ctx = [r.choice([0, 1, r.randint(2, 48), r.randint(49, 400)]) for _ in range(batch)]
+    wgs = r.choice([None, None, 5, 256, 3000])
+    _say("decode large batch", seed, dict(hd=hd, nkv=nkv, groups=groups, bs=bs, dtype=dtype,
+                                          batch=batch, sum_ctx=sum(ctx), wgs=wgs))  # fmt: skip
+    step = workloads.custom(ctx, nkv * groups, nkv, hd, bs, dtype, DEV, seed=seed)
+    args = (step.q, step.k_cache, step.v_cache, step.block_tables, step.context_lens, bs)
+    out32 = torch.empty(step.q.shape, dtype=torch.float32, device=DEV)
+    pa.paged_decode_attention(*args, out=out32, num_workgroups=wgs)
+    torch.cuda.synchronize()
+    want = oracle.decode_attention(step.q.cpu(), step.k_cache.cpu(), step.v_cache.cpu(),
+                                   step.block_tables.cpu(), step.context_lens.cpu(), bs,
+                                   threads=THREADS)  # fmt: skip
+    assert (out32.cpu() - want).abs().max().item() <= ATOL
+
+
 @pytest.mark.parametrize("seed", range(28))
 def test_prefill_random_shape(seed):
     r = random.Random(1000 + seed)
