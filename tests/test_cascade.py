@@ -78,7 +78,8 @@ def test_no_groups_when_nothing_is_shared():
 @pytest.mark.gpu
 @pytest.mark.parametrize("wgs", [None, 1, 7])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize(("nh", "nkv", "hd", "bs"), [(24, 8, 128, 16), (8, 2, 64, 4), (16, 16, 256, 16)])
+@pytest.mark.parametrize(("nh", "nkv", "hd", "bs"), [(24, 8, 128, 16), (8, 2, 64, 4), (16, 16, 256, 16),
+                                                    (8, 4, 32, 16), (16, 4, 64, 32)])  # fmt: skip
 def test_cascade_matches_oracle(dtype, nh, nkv, hd, bs, wgs):
     """The prefix parts merge where each sequence finishes: in the decode kernel itself
     for a sequence one workgroup holds whole (every one of them at wgs=1), in the
