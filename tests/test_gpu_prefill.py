@@ -245,3 +245,29 @@ def test_prefill_many_chunks(n_chunks):
     got = _run(q, k, v, tables, ctx, cu, 16, max(qs))
     want = oracle.prefill_attention(q, k, v, tables, cu, ctx, 16, threads=THREADS)
     assert (got - want).abs().max().item() <= ATOL
+
+
+@pytest.mark.parametrize("hd", [64, 128])
+def test_prefill_bf16_values_beyond_fp16(hd):
+    """For bf16 caches the P.V product takes V as fp16 (converted in LDS as each tile
+    lands); a workgroup whose item meets a V value outside fp16's range recomputes the
+    item with the exact bf16 pair. Some V rows of chunks 0 and 2 are scaled by 3e6 and
+    -7e4 (fp16 would hold them as +-inf): every output is finite and within 2e-3 of the
+    oracle relative to the largest |V| its chunk reads, the other chunks within 2e-3."""
+    _say("prefill bf16 V beyond fp16", hd)
+    spec = [(40, 300), (33, 33), (64, 500), (1, 90)]
+    q, k, v, tables, ctx, cu = _chunks(spec, 8, 2, hd, 16, torch.bfloat16, seed=hd)
+    scale = [1.0] * len(spec)
+    for c, f in ((0, 3e6), (2, -7e4)):
+        blocks = tables[c, : -(-int(ctx[c]) // 16)]
+        rows = (blocks[:, None] * 16 + torch.arange(16)).flatten()[::5]
+        v[rows, :, : hd // 2] = (v[rows, :, : hd // 2].float() * f).to(torch.bfloat16)
+        scale[c] = v[rows].float().abs().max().item()
+    assert scale[0] > 65504 and scale[2] > 65504
+    got = _run(q, k, v, tables, ctx, cu, 16, max(s for s, _ in spec))
+    want = oracle.prefill_attention(q, k, v, tables, cu, ctx, 16, threads=THREADS)
+    assert torch.isfinite(got).all()
+    for c in range(len(spec)):
+        lo, hi = int(cu[c]), int(cu[c + 1])
+        err = (got[lo:hi] - want[lo:hi]).abs().max().item()
+        assert err <= ATOL * scale[c], (c, err, scale[c])
