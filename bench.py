@@ -326,7 +326,9 @@ def bench_cascade(args, torch, step, pools, out, wgs, unique_bytes) -> dict:
     groups = pa.shared_prefixes(tables, step.context_lens.cpu().numpy(), bs)
     if not groups:
         return {"cascade": None}
-    pieces, slots = pa.cascade_pieces(n, nh, nkv, step.q.device), 1  # DecodeGraphs' default
+    pieces = pa.cascade_pieces(n, nh, nkv, step.q.device, dtype=step.k_cache.dtype,
+                               head_dim=step.q.shape[2], block_size=bs)  # fmt: skip
+    slots = 1  # DecodeGraphs' default
     width = -(-w // pieces)
     flat = np.zeros(pa.prefix_entries(n, pieces, slots, width, n), dtype=np.int32)
     groups.sort(key=lambda g: -len(g[0]) * g[1])

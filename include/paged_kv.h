@@ -210,6 +210,46 @@ int pkv_paged_decode_ex(void* out, int out_dtype, int64_t out_stride_b, int64_t 
                         const int32_t* prefix_row, int32_t prefix_parts,
                         int64_t prefix_stride, void* stream);
 
+/* 1 when pkv_cascade_decode runs the prefix pass and the decode pass as one launch for
+ * these shapes (at the library's default workgroup count), else 0. Callers that lay out
+ * prefix groups use it to pick the pieces per prefix (no counterpart in the reference). */
+int32_t pkv_cascade_one_launch(int kv_dtype, int32_t head_dim, int32_t num_heads,
+                               int32_t num_kv_heads, int32_t block_size, int32_t batch);
+
+/*
+ * Cascade decode in one call (no counterpart in the reference, which reads every
+ * sequence's whole context): the prefix pass -- pkv_paged_prefill_ex(prefix_out, PKV_F32,
+ * row stride num_heads * head_dim, head stride head_dim, q, ..., prefix_tables,
+ * prefix_table_stride, prefix_width, prefix_ctx, prefix_cu_q, prefix_chunks,
+ * prefix_max_queries, ..., causal 0, prefix_q_rows, prefix_lse) -- followed by
+ * pkv_paged_decode_ex(out, ..., first_block, lse, prefix_out, prefix_lse, prefix_row,
+ * prefix_parts, prefix_stride), with the same arguments, results and errors as those two
+ * calls. prefix_out (fp32 [rows, num_heads, head_dim], contiguous, 16-byte aligned) and
+ * prefix_lse (fp32 [rows, num_heads]) are the caller's scratch for the parts.
+ * prefix_workgroups < 0 runs the two passes as two launches. Otherwise, for 16-bit K/V at
+ * head_dim 64 or 128, power-of-two blocks of at least 16 tokens, 65 to 1,024 sequences and
+ * at least 8 (KV head, head sub-group) tasks, the two passes share one launch:
+ * prefix_workgroups (0: the library's default) of the num_workgroups workgroups take the
+ * prefix pass's items in turn while the others run the stream pass. Other shapes run two
+ * launches. The workspace is pkv_cascade_workspace_bytes(num_workgroups, ...) bytes, as
+ * for pkv_paged_decode_ex.
+ */
+int pkv_cascade_decode(void* out, int out_dtype, int64_t out_stride_b, int64_t out_stride_h,
+                       const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                       const void* k_cache, const void* v_cache, int kv_dtype,
+                       int64_t kv_stride_slot, int64_t kv_stride_head, int64_t num_slots,
+                       const int32_t* block_tables, int64_t table_stride, int32_t max_blocks,
+                       const int32_t* context_lens, int32_t batch, int32_t num_heads,
+                       int32_t num_kv_heads, int32_t head_dim, int32_t block_size, float scale,
+                       int32_t num_workgroups, void* workspace, int64_t workspace_bytes,
+                       const int32_t* first_block, float* lse, const int32_t* prefix_tables,
+                       int64_t prefix_table_stride, int32_t prefix_width,
+                       const int32_t* prefix_ctx, const int32_t* prefix_cu_q,
+                       int32_t prefix_chunks, int32_t prefix_max_queries,
+                       const int32_t* prefix_q_rows, float* prefix_out, float* prefix_lse,
+                       const int32_t* prefix_row, int32_t prefix_parts, int64_t prefix_stride,
+                       int32_t prefix_workgroups, void* stream);
+
 /*
  * Chunked-prefill attention over the paged pool, on the matrix cores. Replaces the
  * reference's gather of each chunk's context slots plus FlashAttention varlen call

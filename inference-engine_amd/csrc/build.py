@@ -23,7 +23,7 @@ PKG_ROOT = os.path.dirname(HERE)
 REPO = os.path.dirname(PKG_ROOT)
 LIB_DIR = os.path.join(PKG_ROOT, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libpaged_kv.so")
-SOURCES = [os.path.join(HERE, f) for f in ("kv_ops.hip", "decode.hip", "prefill.hip", "fused.hip")]
+SOURCES = [os.path.join(HERE, f) for f in ("kv_ops.hip", "decode.hip", "prefill.hip", "cascade.hip", "fused.hip")]
 INCLUDE = os.path.join(REPO, "include")
 
 HIPCC_FLAGS = [

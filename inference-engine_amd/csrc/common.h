@@ -43,6 +43,12 @@ constexpr int kWave = 64;
 #ifndef PKV_DECODE_COMBINE_SPLIT_PAIRS
 #define PKV_DECODE_COMBINE_SPLIT_PAIRS 2048
 #endif
+// One-launch cascade: the share of the unit stream each prefix workgroup takes after its
+// prefix items, in eighths of a stream workgroup's share (measured at config 3: 2 against
+// 0, 1, 3 and 4).
+#ifndef PKV_CASCADE_TAIL_EIGHTHS
+#define PKV_CASCADE_TAIL_EIGHTHS 2
+#endif
 #ifndef PKV_PREFILL_SETPRIO
 #define PKV_PREFILL_SETPRIO 0
 #endif

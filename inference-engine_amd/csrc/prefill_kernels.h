@@ -1,0 +1,714 @@
+// prefill_kernels.h -- chunked-prefill attention on the matrix cores (gfx950 device
+// code). prefill.hip launches it for chunked prefill and cascade decode's prefix pass;
+// cascade.hip runs the same item code inside the one-launch cascade.
+
+#pragma once
+
+#include "common.h"
+
+namespace pkv {
+
+struct PrefillArgs {
+  void* out;
+  int64_t out_st, out_sh;
+  const void* q;
+  int64_t q_st, q_sh;
+  const void* k;
+  const void* v;
+  int64_t kv_ss, kv_sh, num_slots;
+  const int32_t* tables;
+  int64_t table_stride;
+  int32_t max_blocks;
+  const int32_t* ctx;   // [n_chunks] context tokens (the chunk's own included)
+  const int32_t* cu_q;  // [n_chunks + 1] query row offsets
+  int32_t n_chunks, nh, nkv, groups, bs, bs_shift;
+  int32_t row_blocks;   // 128-row blocks per chunk (static bound)
+  float scale_log2;
+  int out_f32;
+  int32_t causal;         // 0: every query of chunk c sees all its n_c keys
+  const int32_t* q_rows;  // [tokens] or null: query token t reads q row q_rows[t]
+  float* lse;             // [tokens, nh] or null: log2 of each softmax's normaliser
+};
+
+}  // namespace pkv
+
+namespace {
+
+using namespace pkv;
+
+// ---------------------------------------------------------------------------------
+// Chunked-prefill attention on the matrix cores (16-bit K/V, head_dim 32/64/128/256).
+//
+// Chunk c has q_c query tokens (rows cu_q[c] .. cu_q[c+1] of q) and a context of n_c
+// tokens in the paged pool (its own tokens last): query i sits at position n_c - q_c + i
+// and attends to keys 0 .. n_c - q_c + i (bottom-right causal, as the reference's
+// PagedBatch._mixed / varlen path). For KV head g the query rows are (token, head j of
+// g's group) pairs, rho = token * G + j. A workgroup of 8 waves takes 128 of them, one
+// work item, and fills a CU:
+//   * Key halves. Waves 0-3 take the item's first half of 64-key tiles, waves 4-7 the
+//     rest; wave w of each half holds rows 32 w .. 32 w + 31 (two 16-row MFMA tiles), and
+//     the two waves of one SIMD (w and w + 4) belong to different halves. At the end the
+//     halves' softmax states (m, l, O) merge through LDS.
+//   * Ping-pong. The halves run one barrier interval apart, alternating a matrix phase
+//     (P.V of the previous tile, QK^T of this one) with a VALU phase (the K/V loads of
+//     later tiles, the softmax of this one), so each SIMD overlaps one wave's MFMAs with
+//     the other's softmax.
+//   * K and V tiles go from the pool straight into LDS (global_load_lds), three
+//     intervals ahead, the 16-byte chunks of each token row XOR-swizzled by the token
+//     index (conflict-free operand reads).
+//   * S^T = K . Q^T with v_mfma_f32_16x16x32 (K rows from LDS as A, Q rows kept in
+//     VGPRs as B): lane (row n, grp g) gets keys 4g + r of each 16-key block for query
+//     row n. fp32 online softmax per row (cross-row max/sum with permlane16/32 swaps).
+//   * O^T += V^T . P^T: P^T's fragment is the lane's own S^T values (the MFMA's
+//     contraction order over keys is chosen to match), so P needs no lane exchange and
+//     takes the registers S had; V^T comes from two ds_read_b64_tr_b16 transpose reads
+//     per MFMA. The rescale factor of row n lives in the lanes that hold O^T's row n.
+// P enters the second product in the K/V type; for bf16 as a hi + lo pair (fp32-like
+// accuracy), for fp16 rounded once.
+// ---------------------------------------------------------------------------------
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+template <int DT> struct Mfma16x16x32Bits;  // MFMA on raw 16-bit bit patterns
+template <> struct Mfma16x16x32Bits<PKV_BF16> {
+  typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+  typedef __bf16 v2 __attribute__((ext_vector_type(2)));
+  // bf16 keeps 8 significant bits, too few for softmax weights at a 2e-3 output bar, so
+  // P enters the product as hi = bf16(P) plus lo = bf16(P - hi) (two MFMAs).
+  static constexpr bool kSplit = true;
+  __device__ static f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8, a),
+                                                   __builtin_bit_cast(v8, b), c, 0, 0, 0);
+  }
+  // 8 finite fp32 -> hi and lo operand fragments (v_cvt_pk_bf16_f32, round to nearest
+  // even).
+  __device__ static void pack8(const float* p, u32x4& hi, u32x4& lo) {
+    uint32_t h[4], l[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      h[i] = __builtin_bit_cast(uint32_t, v2{(__bf16)p[2 * i], (__bf16)p[2 * i + 1]});
+      // the empty asm keeps h[i] one value (no second conversion to rebuild its low half)
+      uint32_t hv = h[i];
+      __asm__("" : "+v"(hv));
+      const float r0 = p[2 * i] - __uint_as_float(hv << 16);
+      const float r1 = p[2 * i + 1] - __uint_as_float(hv & 0xFFFF0000u);
+      l[i] = __builtin_bit_cast(uint32_t, v2{(__bf16)r0, (__bf16)r1});
+    }
+    hi = u32x4{h[0], h[1], h[2], h[3]};
+    lo = u32x4{l[0], l[1], l[2], l[3]};
+  }
+};
+template <> struct Mfma16x16x32Bits<PKV_F16> {
+  typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+  typedef _Float16 v2 __attribute__((ext_vector_type(2)));
+  static constexpr bool kSplit = false;  // fp16 keeps 11 bits: P rounded once
+  __device__ static f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8, a),
+                                                  __builtin_bit_cast(v8, b), c, 0, 0, 0);
+  }
+  __device__ static void pack8(const float* p, u32x4& hi, u32x4& lo) {
+    uint32_t h[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      h[i] = __builtin_bit_cast(uint32_t, v2{(_Float16)p[2 * i], (_Float16)p[2 * i + 1]});
+    hi = u32x4{h[0], h[1], h[2], h[3]};
+    lo = hi;
+  }
+};
+
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding: vmcnt in
+// bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8). Direct-to-LDS loads count in vmcnt and
+// complete in issue order like every other vector-memory load.
+template <int N> __device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit field");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+// Wait for every outstanding LDS access of this wave.
+__device__ __forceinline__ void wait_lgkm0() {
+  __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// LDS byte address of a __shared__ object.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const lds_void*)p;
+}
+
+// Global memory straight into LDS, one wave at a time: lane i's 16 (4) bytes land at LDS
+// address lds_base + 16 i (+ 4 i); lds_base is wave-uniform and travels in M0. Written
+// as inline asm on purpose: the compiler then neither treats the load as a pending LDS
+// write (which makes it wait for every outstanding load before each later LDS read) nor
+// counts it when it sizes its own vmcnt waits. Kernels that use these issue no other
+// vector-memory loads in the same loop and order everything with wait_vmcnt and
+// barriers themselves.
+__device__ __forceinline__ void dma16_to_lds(const void* src, uint32_t lds_base) {
+  asm volatile("global_load_lds_dwordx4 %0, off" : : "v"(src), "{m0}"(lds_base) : "memory");
+}
+// The same with a wave-uniform 64-bit base in SGPRs and a 32-bit per-lane byte offset.
+__device__ __forceinline__ void dma16_to_lds_s(const void* base, uint32_t off, uint32_t lds_base) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" : : "v"(off), "s"(base), "{m0}"(lds_base)
+               : "memory");
+}
+__device__ __forceinline__ void dma4_to_lds(const void* src, uint32_t lds_base) {
+  asm volatile("global_load_lds_dword %0, off" : : "v"(src), "{m0}"(lds_base) : "memory");
+}
+
+// Wave priority around runs of MFMAs: when two waves share a SIMD, the one about to
+// issue matrix instructions goes first while the other does its softmax arithmetic.
+__device__ __forceinline__ void mfma_phase_begin() {
+#if PKV_PREFILL_SETPRIO
+  __builtin_amdgcn_s_setprio(1);
+#endif
+}
+__device__ __forceinline__ void mfma_phase_end() {
+#if PKV_PREFILL_SETPRIO
+  __builtin_amdgcn_s_setprio(0);
+#endif
+}
+
+template <int HD> struct PrefillShape {
+  static constexpr int RT = HD >= 256 ? 1 : 2;   // 16-row MFMA tiles per wave
+  static constexpr int BM = 4 * 16 * RT;         // query rows per workgroup (4 waves a half)
+  static constexpr int KT = HD >= 256 ? 32 : 64; // keys per tile
+  static constexpr int CH = HD / 8;              // 16-byte granules per K/V row
+  static constexpr int NBETA = KT / 16;          // 16-key blocks of S^T per tile
+  static constexpr int NSG = KT / 32;            // 32-key contraction steps of O^T per tile
+  static constexpr int KS = HD / 32;             // contraction steps over head_dim
+  static constexpr int DTL = HD / 16;            // 16-dim tiles of O^T
+  static constexpr int NLD = KT * CH / 256;      // granules per thread per tile, K and V each
+  static constexpr int TILE = KT * CH;           // granules of one K (or V) tile
+  static_assert(NLD >= 1 && KT * CH % 256 == 0, "tile must split evenly over 256 threads");
+  static_assert(2 * NLD < 64, "vmcnt range");
+  static_assert(KT <= kWave, "a tile's block ids must fit one 64-entry table window");
+  // LDS position of chunk c of key t's row is c ^ swz(t). Rows are 256 bytes (head dim
+  // 128, 16 chunks). With 64 banks (a 256-byte window), a ds_read_b128 serves 16 lanes
+  // and a ds_read_b64 32 lanes per pass: the K operand reads (16 consecutive keys, one
+  // chunk) are conflict-free when swz is a bijection of the key's low 4 bits, the V^T
+  // transpose reads (8 consecutive keys x chunks 2d, 2d + 1 per 32 lanes) when swz's
+  // bits 1-3 are a bijection of the key's bits 0-2. swz(t) = (t3, t0, t1, t2) -- bits
+  // 0..3 -- satisfies both (PKV_PREFILL_SWZ 1; measured at config 5: half the bank-
+  // conflict cycles of the 32-bank layout (t2, t0, t1, t3), same results, same time).
+  __device__ static int swz(int t) {
+#if PKV_PREFILL_SWZ == 1
+    if constexpr (CH == 16) return ((t & 7) << 1) | ((t >> 3) & 1);
+#else
+    if constexpr (CH == 16) return ((t << 1) & 6) | ((t >> 2) & 1) | (t & 8);
+#endif
+    else return t % CH;
+  }
+};
+
+// One work item (chunk, 128-row block, KV head) on a workgroup of 512 threads. Every
+// exit is workgroup-uniform except half 1's after the merge; a caller that runs several
+// items on one workgroup puts a barrier between them (the merge reuses the rings).
+template <int DT, int HD, bool POW2>
+__device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int item) {
+  using SH = PrefillShape<HD>;
+  constexpr int RT = SH::RT, BM = SH::BM, KT = SH::KT, CH = SH::CH, NBETA = SH::NBETA;
+  constexpr int NSG = SH::NSG, KS = SH::KS, DTL = SH::DTL, NLD = SH::NLD, TILE = SH::TILE;
+  static_assert(HD % 32 == 0 && HD <= 256, "head_dim must be 32..256, a multiple of 32");
+  using MMA = Mfma16x16x32Bits<DT>;
+  using S = typename Elt<DT>::S;
+  // ring[half][0 = K, 1 = V][stage]: each key half's K and V tiles, two stages each.
+  __shared__ __align__(16) u32x4 ring[2][2][2][TILE];
+  // Block-table windows, per half and wave, in a ring of three (one per tile in flight).
+  __shared__ __align__(16) int32_t idring[2][3][4][kWave];
+
+  const int tid = threadIdx.x;
+  const int half = __builtin_amdgcn_readfirstlane(tid >> 8);  // which half of the key tiles
+  const int htid = tid & 255;                                 // thread index inside the half
+  const int lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(htid / kWave);  // rows 32 wave .. (RT = 2)
+  const int col = lane & 15, grp = lane >> 4;
+  // Work items (chunk, row block, KV head), heaviest first: chunks by context length
+  // (longest first), then row blocks from the last (it sees the most keys), KV heads
+  // innermost. One workgroup fills a CU, so a grid larger than the GPU runs the items
+  // in this order as CUs free up: the longest start earliest.
+  const int kvh = item % a.nkv;
+  const int rbi = (item / a.nkv) % a.row_blocks;
+  const int crank = item / (a.nkv * a.row_blocks);
+  // Each wave ranks up to 63 chunks by itself; larger batches keep their order. Lane j
+  // fetches chunk j's length and query offset (and lane n_chunks the end offset) in one
+  // round trip, so the chunk's numbers come from the lanes, not a second dependent load.
+  const int cap = a.max_blocks * a.bs;
+  int c = crank, q0, q1, n;
+  if (a.n_chunks < kWave) {
+    const int mine = lane < a.n_chunks ? min(max(a.ctx[lane], 0), cap) : -1;
+    const int cq = lane <= a.n_chunks ? a.cu_q[lane] : 0;
+    int rank = 0;
+    for (int j = 0; j < a.n_chunks; ++j) {
+      const int other = __shfl(mine, j);
+      rank += (other > mine) || (other == mine && j < lane);
+    }
+    const uint64_t hit = __ballot(lane < a.n_chunks && rank == crank);
+    c = __builtin_ctzll(hit);
+    q0 = __builtin_amdgcn_readlane(cq, c);
+    q1 = __builtin_amdgcn_readlane(cq, c + 1);  // c + 1 <= n_chunks < 64
+    n = __builtin_amdgcn_readlane(mine, c);
+  } else {
+    q0 = a.cu_q[c];
+    q1 = a.cu_q[c + 1];
+    n = min(max(a.ctx[c], 0), cap);
+  }
+  const int qlen = q1 - q0;
+  const int G = a.groups;
+  const int nrows = qlen * G;
+  const int rho0 = (a.row_blocks - 1 - rbi) * BM;
+  if (qlen <= 0 || rho0 >= nrows) return;  // uniform per workgroup
+  const int base_pos = n - qlen;  // position of query token 0
+
+  // This lane's query row in each of its wave's 16-row tiles (B operand column). Both
+  // halves hold the same rows.
+  int row_tok[RT];
+  bool row_ok[RT];
+  u32x4 qf[RT][KS];
+#pragma unroll
+  for (int t = 0; t < RT; ++t) {
+    const int rho = rho0 + 16 * RT * wave + 16 * t + col;
+    row_ok[t] = rho < nrows;
+    const int rr = row_ok[t] ? rho : 0;
+    row_tok[t] = rr / G;
+    int64_t qrow = q0 + row_tok[t];
+    if (a.q_rows) {  // a negative entry: no query there (nothing read or written)
+      const int qr = a.q_rows[q0 + row_tok[t]];
+      row_ok[t] = row_ok[t] && qr >= 0;
+      qrow = qr >= 0 ? qr : 0;
+    }
+    const S* qp = reinterpret_cast<const S*>(a.q) + qrow * a.q_st +
+                  (int64_t)(kvh * G + rr % G) * a.q_sh + 8 * grp;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qf[t][s] = *reinterpret_cast<const u32x4*>(qp + 32 * s);
+  }
+  // A row block of padding only (every q_rows entry negative: a fixed-shape layout's
+  // spare rows) leaves before any key tile; the test is workgroup-uniform.
+  if (a.q_rows) {
+    bool any = false;
+#pragma unroll
+    for (int t = 0; t < RT; ++t) any = any || row_ok[t];
+    if (!__syncthreads_or(any)) return;
+  }
+  // Keys any row of this workgroup attends to: [0, kend), in ntiles tiles; half 0 takes
+  // tiles 0 .. ns - 1, half 1 the other ntiles - ns.
+  const int last_row = min(nrows - 1, rho0 + BM - 1);
+  const int kend = a.causal ? min(n, base_pos + last_row / G + 1) : n;
+  const int ntiles = kend > 0 ? (kend + KT - 1) / KT : 0;
+  const int ns = (ntiles + 1) / 2;
+  const int tbeg = half ? ns : 0;
+  const int nt = half ? ntiles - ns : ns;
+
+  // Tile j's K (or V) rows go from the pool straight into LDS. Instruction r of wave w
+  // fills granules r*256 + 64w .. +63 of the tile, one per lane; granule (token t,
+  // position p) holds chunk p ^ swz(t) of that token's row, so the MFMA operand reads
+  // below are conflict-free. Positions past the context re-read the last context token
+  // (finite, masked out of the softmax). The 64 block-table entries from the tile's first
+  // block on reach LDS the same way, two tiles ahead of the K/V loads that need them.
+  // Granule r of this thread: token tok_of(r) of the tile, LDS position chk_of(r).
+  auto tok_of = [&](int r) { return (r * 256 + htid) / CH; };
+  auto chk_of = [&](int r) { return ((r * 256 + htid) % CH) ^ SH::swz(tok_of(r)); };
+  const int32_t* trow = a.tables + (int64_t)c * a.table_stride;
+  const int nlast = max(n - 1, 0);
+  auto blk_of = [&](int p) { return POW2 ? (p >> a.bs_shift) : p / a.bs; };
+  const int blast = blk_of(nlast);
+  const uint32_t ring_lds = lds_addr(&ring[half][0][0][0]);
+  const uint32_t ids_lds = lds_addr(&idring[half][0][wave][0]);
+  // Local tile m of this half is tile tbeg + m; past the half's end, the last one (the
+  // loads keep their count; their stages are free).
+  auto gtile = [&](int m) { return tbeg + min(m, nt - 1); };
+  auto issue_ids = [&](int m) __attribute__((always_inline)) {
+    const int b = min(blk_of(gtile(m) * KT) + lane, blast);
+    dma4_to_lds(trow + b, ids_lds + (uint32_t)((m % 3) * 4 * kWave * 4));
+  };
+  // One DMA instruction of one wave covers SEG consecutive keys of a tile. When the block
+  // size is a power of two >= SEG those keys share one block: its id is wave-uniform and
+  // the address is scalar math plus one per-lane offset.
+  constexpr int SEG = kWave / CH;
+  const bool seg_uniform = POW2 && a.bs >= SEG;
+  // Fast path (power-of-two blocks of at least SEG keys, tile inside the context): the
+  // lane's byte offset inside its block is the same for every tile, plus a uniform part
+  // when blocks are longer than a tile.
+  uint32_t lane_off[NLD];
+#pragma unroll
+  for (int r = 0; r < NLD; ++r)
+    lane_off[r] = (uint32_t)(((tok_of(r) & (a.bs - 1)) * a.kv_ss + chk_of(r) * 8) * (int64_t)sizeof(S));
+  const int64_t blk_bytes = (int64_t)a.bs * a.kv_ss * (int64_t)sizeof(S);
+  const int64_t kvh_bytes = (int64_t)kvh * a.kv_sh * (int64_t)sizeof(S);
+  // Per round only a 32 x 32-bit multiply-add in SGPRs: block bytes must fit 32 bits
+  // (they do for any real pool), block ids past the pool read block 0.
+  const bool fast = seg_uniform && blk_bytes <= 0xFFFFFFFFll;
+  const uint32_t blk_bytes32 = (uint32_t)blk_bytes;
+  const uint32_t pool_blocks = (uint32_t)min(a.num_slots / a.bs, (int64_t)0x7FFFFFFF);
+  const char* kv_base[2] = {reinterpret_cast<const char*>(a.k) + kvh_bytes,
+                            reinterpret_cast<const char*>(a.v) + kvh_bytes};
+  // K (kv = 0) or V (kv = 1) of local tile m into stage m % 2.
+  auto issue_tile = [&](int m, int kv) __attribute__((always_inline)) {
+    const int j = gtile(m);
+    const int32_t* ids = &idring[half][m % 3][wave][0];
+    const int b0 = blk_of(j * KT);
+    const char* src = reinterpret_cast<const char*>(kv ? a.v : a.k);
+    const uint32_t dst = ring_lds + (uint32_t)(((kv * 2 + (m & 1)) * TILE) * 16);
+    if constexpr (POW2) {
+      if (fast && (j + 1) * KT <= n) {
+        int id[NLD];
+#pragma unroll
+        for (int r = 0; r < NLD; ++r)  // every id read before the first DMA
+          id[r] = ids[((j * KT + (r * 256 + wave * kWave) / CH) >> a.bs_shift) - b0];
+        const char* base = kv_base[kv] + (uint32_t)(((j * KT) & (a.bs - 1)) * a.kv_ss * (int)sizeof(S));
+#pragma unroll
+        for (int r = 0; r < NLD; ++r) {
+          uint32_t bid = (uint32_t)__builtin_amdgcn_readfirstlane(id[r]);
+          bid = bid < pool_blocks ? bid : 0u;  // memory safety only
+          dma16_to_lds_s(base + (uint64_t)bid * blk_bytes32, lane_off[r],
+                         dst + (uint32_t)((r * 256 + wave * kWave) * 16));
+        }
+        return;
+      }
+      if (seg_uniform) {  // the context's last tile: positions past it re-read its last token
+        int id[NLD];
+#pragma unroll
+        for (int r = 0; r < NLD; ++r) {  // every id read before the first DMA
+          const int seg = j * KT + (r * 256 + wave * kWave) / CH;  // first key, uniform
+          id[r] = ids[min(seg >> a.bs_shift, blast) - b0];
+        }
+#pragma unroll
+        for (int r = 0; r < NLD; ++r) {
+          const int seg = j * KT + (r * 256 + wave * kWave) / CH;
+          const int blk = min(seg >> a.bs_shift, blast);
+          int64_t bid = __builtin_amdgcn_readfirstlane(id[r]);
+          if (bid < 0 || (bid + 1) * a.bs > a.num_slots) bid = 0;  // memory safety only
+          const int64_t base = (bid * a.bs * a.kv_ss + (int64_t)kvh * a.kv_sh) * (int64_t)sizeof(S);
+          const int in_blk = min(seg + lane / CH, nlast) - blk * a.bs;
+          const uint32_t lo = (uint32_t)((in_blk * a.kv_ss + chk_of(r) * 8) * (int64_t)sizeof(S));
+          dma16_to_lds(src + base + lo, dst + (uint32_t)((r * 256 + wave * kWave) * 16));
+        }
+        return;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < NLD; ++r) {
+      const int p = min(j * KT + tok_of(r), nlast);
+      const int blk = blk_of(p);
+      int64_t sl = (int64_t)ids[blk - b0] * a.bs + (p - blk * a.bs);
+      sl = (sl >= 0 && sl < a.num_slots) ? sl : 0;
+      const int64_t off = (sl * a.kv_ss + (int64_t)kvh * a.kv_sh + chk_of(r) * 8) * (int64_t)sizeof(S);
+      dma16_to_lds(src + off, dst + (uint32_t)((r * 256 + wave * kWave) * 16));
+    }
+  };
+
+  float m_run[RT], l_run[RT];
+  f32x4 o[RT][DTL];
+#pragma unroll
+  for (int t = 0; t < RT; ++t) {
+    m_run[t] = -INFINITY;
+    l_run[t] = 0.f;
+#pragma unroll
+    for (int d = 0; d < DTL; ++d) o[t][d] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // Rows whose causal limit a tile can cross: tile j needs the mask only if it reaches
+  // past the smallest limit among this workgroup's rows (its first row's).
+  const int limit_min = a.causal ? min(n - 1, base_pos + rho0 / G) : n - 1;
+  const int j_mask = min(ntiles, max(0, (limit_min + 1) / KT));
+  int limit[RT];  // last key each of this lane's rows sees
+#pragma unroll
+  for (int t = 0; t < RT; ++t) limit[t] = a.causal ? min(n - 1, base_pos + row_tok[t]) : n - 1;
+
+  // Per-lane LDS byte offsets of the operand fragments inside a tile, recomputed where
+  // they are used (a few VALU instructions; holding them would cost 12 registers).
+  //   K: lane (col, grp) reads key 16 beta + col, chunk 4 s + grp. swz(key) depends on
+  //      beta only when a row has more than 16 chunks (head_dim 256).
+  //   V^T: lane (col, grp) reads key 32 sg + 16 h2 + 4 grp + col / 4, dims 16 d +
+  //      4 (col % 4) .. +4 (chunk 2 d + (col % 4) / 2, half (col % 4) & 1).
+  constexpr int KSW = CH > 16 ? NBETA : 1;
+  constexpr int VSW = CH > 16 ? 2 : 1;
+  auto fresh_lane = [&]() {  // lane, as a value the compiler must not hoist
+    int l = lane;
+    __asm__ volatile("" : "+v"(l));
+    return l;
+  };
+  auto koff = [&](int l, int b, int s) {
+    const int tk = 16 * b + (l & 15);
+    return (uint32_t)(((4 * s + (l >> 4)) ^ SH::swz(tk)) * 16 + (l & 15) * CH * 16);
+  };
+  auto voff = [&](int l, int h2, int d) {
+    const int c4 = l & 3, tr = 4 * (l >> 4) + ((l & 15) >> 2);
+    const int tk = 16 * h2 + tr;
+    return (uint32_t)((((2 * d + c4 / 2) ^ SH::swz(tk)) * 16 + (c4 & 1) * 8) + tr * CH * 16);
+  };
+
+  // S^T of a tile from its QK^T to its softmax, then in the same registers its
+  // probabilities P^T until its P.V (the first 32-key step's already packed as operand
+  // fragments: hi in block 0, lo in block 1).
+  static_assert(NBETA == 2 * NSG, "two score blocks per P^T fragment pair");
+  f32x4 sc[RT][NBETA];
+
+  // S^T = K . Q^T of local tile m: block beta holds keys 16 beta + 4 grp + r for query
+  // row col.
+  auto qk = [&](int m) __attribute__((always_inline)) {
+    const char* stage = reinterpret_cast<const char*>(&ring[half][0][m & 1][0]);
+    const int l = fresh_lane();
+#pragma unroll
+    for (int beta = 0; beta < NBETA; ++beta) {
+      if (beta) __builtin_amdgcn_sched_barrier(0);  // one 16-key block's K fragments at a time
+#pragma unroll
+      for (int t = 0; t < RT; ++t) sc[t][beta] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const u32x4 kf = *reinterpret_cast<const u32x4*>(stage + beta * 16 * CH * 16 +
+                                                         koff(l, KSW == 1 ? 0 : beta, s));
+#pragma unroll
+        for (int t = 0; t < RT; ++t) sc[t][beta] = MMA::mma(kf, qf[t][s], sc[t][beta]);
+      }
+    }
+  };
+  // O^T += V^T . P^T of local tile m; each V^T fragment (two ds_read_b64_tr_b16
+  // transpose reads) serves every row tile. P arrives as fp32 probabilities; each 32-key
+  // step packs its operand fragments here, in the matrix phase, whose VALU is otherwise
+  // idle (the softmax phase is the longer one).
+  auto pv = [&](int m) __attribute__((always_inline)) {
+    const char* vstage = reinterpret_cast<const char*>(&ring[half][1][m & 1][0]);
+    const int l = fresh_lane();
+#pragma unroll
+    for (int sg = 0; sg < NSG; ++sg) {
+      if (sg) __builtin_amdgcn_sched_barrier(0);  // one 32-key step's fragments at a time
+      // P^T fragment of row tile t: the lane's own 8 probabilities (keys 32 sg + 16
+      // (e / 4) + 4 grp + e % 4), matching the transpose-read order of V^T. Step 0 was
+      // packed by the softmax; the later steps are packed here, while step 0's MFMAs run.
+      u32x4 phi[RT], plo[RT];
+#pragma unroll
+      for (int t = 0; t < RT; ++t) {
+        if (sg == 0) {
+          phi[t] = __builtin_bit_cast(u32x4, sc[t][0]);
+          plo[t] = __builtin_bit_cast(u32x4, sc[t][1]);
+        } else {
+          float p8[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) p8[e] = sc[t][2 * sg + e / 4][e % 4];
+          MMA::pack8(p8, phi[t], plo[t]);
+        }
+      }
+#pragma unroll
+      for (int d = 0; d < DTL; ++d) {
+        u32x4 vf;
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+          // generic -> LDS address space (an addrspacecast of a __shared__ pointer)
+          const s16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_s16x4*)(vstage + (32 * sg + 16 * h2) * CH * 16 + voff(l, VSW == 1 ? 0 : h2, d)));
+          const uint32_t lo = (uint32_t)(uint16_t)x[0] | ((uint32_t)(uint16_t)x[1] << 16);
+          const uint32_t hi = (uint32_t)(uint16_t)x[2] | ((uint32_t)(uint16_t)x[3] << 16);
+          if (h2 == 0) { vf.x = lo; vf.y = hi; } else { vf.z = lo; vf.w = hi; }
+        }
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+          o[t][d] = MMA::mma(vf, phi[t], o[t][d]);
+          if constexpr (MMA::kSplit) o[t][d] = MMA::mma(vf, plo[t], o[t][d]);
+        }
+      }
+    }
+  };
+  // Online softmax of global tile j's scores into P^T fragments; masked: some key of the
+  // tile is past some row's causal limit (the tiles on the diagonal and the context end;
+  // a wave-uniform branch around the mask only: one copy of the rest, whose registers a
+  // second copy would double).
+  auto softmax = [&](int j, bool masked) __attribute__((always_inline)) {
+    const int kt0 = j * KT;
+    // p = exp2(scale_log2 * s - m_run). The reference m_run is raised only when a score
+    // exceeds it by more than 2^8: a stale reference changes nothing in O / l (both carry
+    // the same factor), keeps p <= 256, and leaves O untouched on most tiles. The row
+    // tiles are independent chains: maxima first, one rescale branch, then every exp.
+    float mx[RT];
+    bool raise[RT];
+    bool any = false;
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+      if (masked) {
+        const int lim = limit[t] - kt0 - 4 * grp;  // keys 16 beta + r past it are out
+#pragma unroll
+        for (int beta = 0; beta < NBETA; ++beta)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (16 * beta + r > lim) sc[t][beta][r] = -INFINITY;
+      }
+      float x = -INFINITY;
+#pragma unroll
+      for (int beta = 0; beta < NBETA; ++beta)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) x = fmaxf(x, sc[t][beta][r]);
+      mx[t] = rows_max(x) * a.scale_log2;
+      raise[t] = mx[t] > m_run[t] + 8.f;  // also true the first time (m_run = -inf)
+      any = any || raise[t];
+    }
+    if (__builtin_amdgcn_ballot_w64(any)) {  // wave-uniform
+#pragma unroll
+      for (int t = 0; t < RT; ++t) {
+        // Rows that do not raise keep their factor 1 (their m_run may still be -inf: a
+        // half's tiles can all lie past a row's causal limit).
+        const float alpha = raise[t] ? __builtin_amdgcn_exp2f(m_run[t] - mx[t]) : 1.f;
+        m_run[t] = raise[t] ? mx[t] : m_run[t];
+        l_run[t] *= alpha;
+#pragma unroll
+        for (int d = 0; d < DTL; ++d) o[t][d] *= alpha;
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+      const float mref = m_run[t] == -INFINITY ? 0.f : m_run[t];
+      float psum = 0.f;
+#pragma unroll
+      for (int beta = 0; beta < NBETA; ++beta)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {  // probabilities replace the scores
+          const float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[t][beta][r], a.scale_log2, -mref));
+          sc[t][beta][r] = pr;
+          psum += pr;
+        }
+      // The first 32-key step's P^T fragments are packed here (hi and lo into score
+      // blocks 0 and 1); P.V packs the others, balancing the two phases.
+      {
+        float p8[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) p8[e] = sc[t][e / 4][e % 4];
+        u32x4 hi, lo;
+        MMA::pack8(p8, hi, lo);
+        sc[t][0] = __builtin_bit_cast(f32x4, hi);
+        sc[t][1] = __builtin_bit_cast(f32x4, lo);
+      }
+      l_run[t] += psum;
+    }
+  };
+
+  // Ping-pong schedule. Interval k (k = 0 .. 2 ns + 1) starts at a workgroup barrier; a
+  // half is at local phase p = k - half, so when one half issues matrix work the other
+  // does its softmax, and each SIMD (one wave of each half) overlaps the two.
+  //   p = 2m (matrix phase):  P.V of tile m - 1, QK^T of tile m.
+  //   p = 2m + 1 (VALU phase): loads of block ids (tile m + 3), V (m + 1), K (m + 2);
+  //                            softmax of tile m.
+  // A K tile is used at phase 2m, its V at 2m + 2; both were issued at 2m - 3, into the
+  // stage that tile m - 2 freed at 2m - 2. Before each matrix phase a wave waits for all
+  // but the loads of the previous VALU phase (2 NLD + 1), before each VALU phase for
+  // all but that phase's K and V loads (its block ids must be in). Loads complete in
+  // issue order.
+  if (nt > 0) {  // prologue: block ids of tiles 0-2, K of 0 and 1, V of 0
+    issue_ids(0);
+    issue_ids(1);
+    wait_vmcnt<0>();
+    issue_tile(0, 0);
+    issue_ids(2);
+    issue_tile(0, 1);
+    issue_tile(1, 0);
+    wait_vmcnt<0>();
+  }
+  // Matrix phase of iteration m and VALU phase of iteration m, each closed by its
+  // barrier. Half 0 runs intervals (M0 V0)(M1 V1)..(M_ns V_ns); half 1 one interval
+  // later: idle, (M0 V0)..(M_ns-1 V_ns-1) M_ns. Both pass 2 ns + 2 barriers.
+  auto interval_m = [&](int m) __attribute__((always_inline)) {
+    if (m >= 1 && m - 1 < nt) wait_vmcnt<2 * NLD + 1>();
+    else wait_vmcnt<0>();
+    wait_lgkm0();
+    __builtin_amdgcn_s_barrier();
+    mfma_phase_begin();
+    if (m >= 1 && m - 1 < nt) pv(m - 1);  // first: P's registers then hold S
+    // Nothing crosses: the V^T and K fragments of the two products are never all live.
+    __builtin_amdgcn_sched_barrier(0);
+    if (m < nt) qk(m);
+    mfma_phase_end();
+  };
+  auto interval_v = [&](int m) __attribute__((always_inline)) {
+    if (m < nt) wait_vmcnt<2 * NLD>();
+    wait_lgkm0();
+    __builtin_amdgcn_s_barrier();
+    if (m >= nt) return;
+    issue_ids(m + 3);
+    issue_tile(m + 1, 1);
+    issue_tile(m + 2, 0);
+    softmax(tbeg + m, tbeg + m >= j_mask);
+  };
+  if (half == 0) {
+    for (int m = 0; m <= ns; ++m) {
+      interval_m(m);
+      interval_v(m);
+    }
+  } else {
+    wait_lgkm0();
+    __builtin_amdgcn_s_barrier();
+    for (int m = 0; m < ns; ++m) {
+      interval_m(m);
+      interval_v(m);
+    }
+    interval_m(ns);
+  }
+
+  // Merge the halves' softmax states through LDS (the rings are free now): half 1
+  // writes (m, l, O) per lane, half 0 reads its partner lane's (same rows, same lane
+  // layout) and scales both by 2^(m_half - max).
+  constexpr int NE = RT * (2 + 4 * DTL);  // floats per lane
+  static_assert(4 * NE * kWave * 4 <= (int)sizeof(ring), "merge exchange must fit the rings");
+  float* xch = reinterpret_cast<float*>(&ring[0][0][0][0]) + wave * NE * kWave + lane;
+  // The last VALU phases issued loads nothing waited for (past the half's end, into
+  // free stages); they must land before the rings are reused.
+  wait_vmcnt<0>();
+  __syncthreads();
+  if (half) {
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+      float* x = xch + t * (2 + 4 * DTL) * kWave;
+      x[0] = m_run[t];
+      x[kWave] = l_run[t];
+#pragma unroll
+      for (int d = 0; d < DTL; ++d)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) x[(2 + 4 * d + r) * kWave] = o[t][d][r];
+    }
+  }
+  __syncthreads();
+  if (half) return;
+#pragma unroll
+  for (int t = 0; t < RT; ++t) {
+    const float* x = xch + t * (2 + 4 * DTL) * kWave;
+    const float mb = x[0];
+    const float mn = fmaxf(m_run[t], mb);
+    const float mref = mn == -INFINITY ? 0.f : mn;  // both empty: weights 0
+    const float sa = __builtin_amdgcn_exp2f(m_run[t] - mref);
+    const float sb = __builtin_amdgcn_exp2f(mb - mref);
+    m_run[t] = mn;
+    l_run[t] = l_run[t] * sa + x[kWave] * sb;
+#pragma unroll
+    for (int d = 0; d < DTL; ++d)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[t][d][r] = o[t][d][r] * sa + x[(2 + 4 * d + r) * kWave] * sb;
+  }
+
+  // O^T lane (row col, grp) holds dims 16 d + 4 grp + r of query row col.
+#pragma unroll
+  for (int t = 0; t < RT; ++t) {
+    const float l_tot = rows_sum(l_run[t]);
+    if (!row_ok[t]) continue;
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    const int rho = rho0 + 16 * RT * wave + 16 * t + col;
+    if (a.lse && grp == 0)  // log2 normaliser: the exponent reference m_run plus log2(sum)
+      a.lse[(int64_t)(q0 + rho / G) * a.nh + kvh * G + rho % G] =
+          l_tot > 0.f ? m_run[t] + __log2f(l_tot) : -INFINITY;
+    const int64_t e0 = (int64_t)(q0 + rho / G) * a.out_st + (int64_t)(kvh * G + rho % G) * a.out_sh;
+#pragma unroll
+    for (int d = 0; d < DTL; ++d) {
+      const int64_t e = e0 + 16 * d + 4 * grp;
+      const float v4[4] = {o[t][d][0] * inv, o[t][d][1] * inv, o[t][d][2] * inv, o[t][d][3] * inv};
+      if (a.out_f32) {
+        *reinterpret_cast<float4*>((float*)a.out + e) = make_float4(v4[0], v4[1], v4[2], v4[3]);
+      } else {
+        *reinterpret_cast<uint2*>((S*)a.out + e) =
+            make_uint2((uint32_t)Elt<DT>::from_f32(v4[0]) | ((uint32_t)Elt<DT>::from_f32(v4[1]) << 16),
+                       (uint32_t)Elt<DT>::from_f32(v4[2]) | ((uint32_t)Elt<DT>::from_f32(v4[3]) << 16));
+      }
+    }
+  }
+}
+template <int DT, int HD, bool POW2>
+__global__ void __launch_bounds__(512)
+paged_prefill_kernel(const PrefillArgs a) {
+  prefill_item<DT, HD, POW2>(a, (int)blockIdx.x);
+}
+
+}  // namespace

@@ -18,7 +18,7 @@ LIB_PATH = os.path.join(
     "lib",
     "libpaged_kv.so",
 )
-ABI_VERSION = 3
+ABI_VERSION = 4
 PKV_NOALLOC_SCRATCH_BYTES = 32 << 20  # include/paged_kv.h
 
 PKV_F32, PKV_F16, PKV_BF16 = 0, 1, 2
@@ -75,6 +75,21 @@ SIGNATURES: dict[str, tuple] = {
          _p, _p,                                  # first_block, lse
          _p, _p, _p, _i32, _i64,                  # prefix out, lse, row, parts, stride
          _p],                                     # stream
+    ),  # fmt: skip
+    "pkv_cascade_one_launch": (_i32, [ctypes.c_int, _i32, _i32, _i32, _i32, _i32]),
+    "pkv_cascade_decode": (
+        ctypes.c_int,
+        [_p, ctypes.c_int, _i64, _i64,            # out
+         _p, _i64, _i64,                          # q
+         _p, _p, ctypes.c_int, _i64, _i64, _i64,  # k, v caches
+         _p, _i64, _i32,                          # block tables
+         _p, _i32, _i32, _i32, _i32, _i32,        # ctx, batch, nh, nkv, hd, bs
+         _f32, _i32, _p, _i64,                    # scale, wgs, workspace
+         _p, _p,                                  # first_block, lse
+         _p, _i64, _i32,                          # prefix tables, stride, width
+         _p, _p, _i32, _i32, _p,                  # prefix ctx, cu_q, chunks, max queries, q_rows
+         _p, _p, _p, _i32, _i64,                  # prefix out, lse, row, parts, stride
+         _i32, _p],                               # prefix workgroups, stream
     ),  # fmt: skip
     "pkv_paged_prefill_ex": (
         ctypes.c_int,

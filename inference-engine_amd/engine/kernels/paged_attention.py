@@ -177,13 +177,17 @@ def find_prefix_groups(block_tables: Sequence[Sequence[int]] | torch.Tensor,
                        context_lens: Sequence[int] | torch.Tensor, block_size: int,
                        num_heads: int, num_kv_heads: int, device: torch.device, *,
                        min_blocks: int = 16, target_workgroups: int | None = None,
-                       pieces: int | None = None) -> PrefixGroups | None:  # fmt: skip
+                       pieces: int | None = None, dtype: torch.dtype | None = None,
+                       head_dim: int | None = None) -> PrefixGroups | None:  # fmt: skip
     """The ``shared_prefixes`` groups of a decode batch laid out for cascade decode
     (host-side, from the tables the engine's block manager produced); None when no group
     qualifies. Each prefix is cut into K pieces (K >= 1, pieces of at least 4 blocks),
-    K = ``pieces`` if given, else the most whose prefix pass has at most
-    ``target_workgroups`` workgroups (default: the GPU's CU count, one workgroup per
-    CU -- a second per CU shares the same matrix cores and only adds parts to merge)."""
+    K = ``pieces`` if given. Otherwise, when the cache's ``dtype`` and ``head_dim`` are
+    given and the library runs these shapes' prefix and decode passes as one launch, K is
+    ``one_launch_pieces`` of the prefix pass's work items; else K is the most whose
+    prefix pass has at most ``target_workgroups`` workgroups (default: the GPU's CU
+    count, one workgroup per CU -- a second per CU shares the same matrix cores and only
+    adds parts to merge)."""
     tables = torch.as_tensor(block_tables, dtype=torch.int32).cpu().numpy()
     ctx = torch.as_tensor(context_lens, dtype=torch.int64).cpu().numpy()
     groups = shared_prefixes(tables, ctx, block_size, min_blocks)
@@ -196,10 +200,14 @@ def find_prefix_groups(block_tables: Sequence[Sequence[int]] | torch.Tensor,
     max_members = max(sizes)
     dev = torch.device(device)
     if pieces is None:
-        if target_workgroups is None:
-            target_workgroups = _cu_count(dev)
         per_piece = _prefix_workgroups(max_members, num_heads // num_kv_heads, num_kv_heads)
-        pieces = target_workgroups // (per_piece * g_count)
+        if dtype is not None and head_dim is not None and \
+                cascade_one_launch(dtype, head_dim, num_heads, num_kv_heads, block_size, b, dev):  # fmt: skip
+            pieces = one_launch_pieces(per_piece * g_count, dev)
+        else:
+            if target_workgroups is None:
+                target_workgroups = _cu_count(dev)
+            pieces = target_workgroups // (per_piece * g_count)
     pieces = max(1, min(pieces, min(sh for _, sh in groups) // 4))
     width = max(-(-shared // pieces) for _, shared in groups)
     host = np.zeros(prefix_entries(b, pieces, g_count, width, s_total), dtype=np.int32)
@@ -219,11 +227,38 @@ def _prefix_workgroups(members: int, groups: int, num_kv_heads: int) -> int:
     return max(1, -(-members * groups // 128) * num_kv_heads)
 
 
+def cascade_one_launch(dtype: torch.dtype, head_dim: int, num_heads: int, num_kv_heads: int,
+                       block_size: int, batch: int, device: torch.device) -> bool:  # fmt: skip
+    """Whether cascade decode of ``batch`` sequences at these shapes runs its prefix pass
+    and decode pass as one launch on ``device`` (``pkv_cascade_one_launch``)."""
+    code = _native.DTYPE_CODE.get(dtype)
+    if torch.device(device).type != "cuda" or code is None:
+        return False
+    return _native.lib().pkv_cascade_one_launch(code, head_dim, num_heads, num_kv_heads,
+                                                block_size, batch) == 1  # fmt: skip
+
+
+def one_launch_pieces(items: int, device: torch.device, max_pieces: int = 8) -> int:
+    """Pieces per prefix for the one-launch cascade, whose prefix pass has ``items`` work
+    items per piece: about 7/32 of the GPU's workgroups in items, one per prefix
+    workgroup (measured on 256 CUs at 96-512 sequences sharing a 2,048-token prefix)."""
+    target = 7 * _cu_count(torch.device(device)) / 32
+    return max(1, min(max_pieces, round(target / max(1, items))))
+
+
 def cascade_pieces(batch: int, num_heads: int, num_kv_heads: int, device: torch.device,
-                   max_pieces: int = 8) -> int:  # fmt: skip
-    """Pieces per shared prefix for a captured step of ``batch`` sequences: as many as
-    keep one group's prefix pass within one workgroup per CU (at most ``max_pieces``)."""
+                   max_pieces: int = 8, *, dtype: torch.dtype | None = None,
+                   head_dim: int | None = None, block_size: int | None = None) -> int:  # fmt: skip
+    """Pieces per shared prefix for a captured step of ``batch`` sequences. With the
+    cache's ``dtype``, ``head_dim`` and ``block_size`` given and a one-launch cascade
+    for these shapes: ``one_launch_pieces`` of one group's prefix items; else as many
+    as keep one group's prefix pass within one workgroup per CU (at most
+    ``max_pieces``)."""
     per_piece = _prefix_workgroups(batch, num_heads // num_kv_heads, num_kv_heads)
+    if dtype is not None and head_dim is not None and block_size is not None and \
+            cascade_one_launch(dtype, head_dim, num_heads, num_kv_heads, block_size, batch,
+                               device):  # fmt: skip
+        return one_launch_pieces(per_piece, device, max_pieces)
     return max(1, min(max_pieces, _cu_count(torch.device(device)) // per_piece))
 
 
@@ -312,6 +347,7 @@ def paged_decode_attention(
     num_workgroups: int | None = None,
     workspace: torch.Tensor | None = None,
     prefix_groups: PrefixGroups | None = None,
+    prefix_workgroups: int | None = None,
 ) -> torch.Tensor:
     """q: [B, nh, hd]; k_cache, v_cache: [num_slots, nkv, hd] (one layer);
     block_tables: [B, max_blocks] int32; context_lens: [B] int32 -> [B, nh, hd].
@@ -330,7 +366,10 @@ def paged_decode_attention(
     members on the matrix cores (the chunked-prefill kernel, non-causal, one fp32 part
     per piece with its log-sum-exp), then the decode kernel reads only each sequence's
     private blocks and merges the parts into its softmax as it finishes each sequence.
-    Other shapes ignore it (the plain decode is exact).
+    Other shapes ignore it (the plain decode is exact). Where the shapes allow it, the
+    prefix pass and the decode pass share one launch: ``prefix_workgroups`` of the
+    workgroups (None: the library's default) take the prefix items while the others
+    stream the private blocks; a negative value runs them as two launches.
     """
     del block_n
     what = "paged_decode_attention"
@@ -370,8 +409,7 @@ def paged_decode_attention(
         ws = workspace
     elif ws_bytes:
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-    pre = _cascade_prefix(q, k_cache, v_cache, block_size, prefix_groups) if cascade else None
-    status = lib.pkv_paged_decode_ex(
+    common = (
         out.data_ptr(), _native.dtype_code(out.dtype, what), out.stride(0), out.stride(1),
         q.data_ptr(), q.stride(0), q.stride(1),
         k_cache.data_ptr(), v_cache.data_ptr(), kv_code,
@@ -379,12 +417,23 @@ def paged_decode_attention(
         block_tables.data_ptr(), block_tables.stride(0), max_blocks,
         context_lens.data_ptr(), b, nh, nkv, hd, block_size,
         hd**-0.5, wg_arg, ws.data_ptr() if ws is not None else None, ws_bytes,
-        prefix_groups.first_block.data_ptr() if cascade else None, None,
-        pre[0].data_ptr() if cascade else None, pre[1].data_ptr() if cascade else None,
-        prefix_groups.prefix_row.data_ptr() if cascade else None,
-        prefix_groups.pieces if cascade else 0, prefix_groups.members if cascade else 0,
-        _native.stream_of(dev),
     )  # fmt: skip
+    if cascade:
+        pg = prefix_groups
+        rows = pg.pieces * pg.members
+        o_pre = torch.empty(rows, nh, hd, dtype=torch.float32, device=dev)
+        lse_pre = torch.empty(rows, nh, dtype=torch.float32, device=dev)
+        pwg = 0 if prefix_workgroups is None else prefix_workgroups
+        status = lib.pkv_cascade_decode(
+            *common, pg.first_block.data_ptr(), None,
+            pg.tables.data_ptr(), pg.tables.stride(0), pg.tables.shape[1],
+            pg.ctx.data_ptr(), pg.cu_q.data_ptr(), pg.ctx.numel(), pg.max_members,
+            pg.q_rows.data_ptr(), o_pre.data_ptr(), lse_pre.data_ptr(),
+            pg.prefix_row.data_ptr(), pg.pieces, pg.members, pwg, _native.stream_of(dev),
+        )  # fmt: skip
+    else:
+        status = lib.pkv_paged_decode_ex(*common, None, None, None, None, None, 0, 0,
+                                         _native.stream_of(dev))  # fmt: skip
     _native.check(status, what)
     return out
 
@@ -488,32 +537,6 @@ def _check_prefix_groups(pg: PrefixGroups, batch: int, dev: torch.device, what: 
             pg.cu_q.shape != (chunks + 1,) or pg.tables.dim() != 2 or \
             pg.tables.shape[0] != chunks or pg.q_rows.shape != (pg.pieces * pg.members,):  # fmt: skip
         raise ValueError(f"{what}: prefix_groups fields disagree with each other")
-
-
-def _cascade_prefix(q, k_cache, v_cache, block_size,
-                    pg: PrefixGroups) -> tuple[torch.Tensor, torch.Tensor]:  # fmt: skip
-    """Prefix pass of cascade decode: every group's queries against its shared blocks,
-    non-causal chunks on the chunked-prefill kernel -> fp32 parts [K * S, nh, hd] and
-    their log2 normalisers [K * S, nh]."""
-    what = "paged_decode_attention (cascade)"
-    nh, hd = q.shape[1], q.shape[2]
-    nkv = k_cache.shape[1]
-    dev = q.device
-    rows = pg.pieces * pg.members
-    o_pre = torch.empty(rows, nh, hd, dtype=torch.float32, device=dev)
-    lse_pre = torch.empty(rows, nh, dtype=torch.float32, device=dev)
-    status = _native.lib().pkv_paged_prefill_ex(
-        o_pre.data_ptr(), _native.PKV_F32, o_pre.stride(0), o_pre.stride(1),
-        q.data_ptr(), q.stride(0), q.stride(1),
-        k_cache.data_ptr(), v_cache.data_ptr(), _native.dtype_code(k_cache.dtype, what),
-        k_cache.stride(0), k_cache.stride(1), k_cache.shape[0],
-        pg.tables.data_ptr(), pg.tables.stride(0), pg.tables.shape[1],
-        pg.ctx.data_ptr(), pg.cu_q.data_ptr(), pg.ctx.numel(), pg.max_members,
-        nh, nkv, hd, block_size, hd**-0.5, 0, pg.q_rows.data_ptr(), lse_pre.data_ptr(),
-        _native.stream_of(dev),
-    )  # fmt: skip
-    _native.check(status, what)
-    return o_pre, lse_pre
 
 
 def reference_decode_attention(

@@ -69,7 +69,8 @@ class DecodeGraphs:
         if cascade:
             nkv = cache.k.shape[2]
             for n in self.sizes:
-                k = pa.cascade_pieces(n, num_heads, nkv, dev)
+                k = pa.cascade_pieces(n, num_heads, nkv, dev, dtype=cache.k.dtype,
+                                      head_dim=cache.k.shape[-1], block_size=cache.block_size)  # fmt: skip
                 self._shape[n] = (k, max_groups, -(-w // k))
                 pre = max(pre, pa.prefix_entries(n, *self._shape[n], n))
         self._pre_len = pre

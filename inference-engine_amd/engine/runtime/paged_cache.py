@@ -274,7 +274,8 @@ class PagedBatch:
 
                 batch.prefix_groups = find_prefix_groups(
                     cls._tables(block_tables), list(context_lens), cache.block_size,
-                    num_heads, cache.k.shape[2], device, min_blocks=cascade_min_blocks)  # fmt: skip
+                    num_heads, cache.k.shape[2], device, min_blocks=cascade_min_blocks,
+                    dtype=cache.k.dtype, head_dim=cache.k.shape[-1])  # fmt: skip
             return batch
         return cls._mixed(cache, block_tables, context_lens, query_lens, device)
 

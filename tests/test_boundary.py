@@ -117,6 +117,40 @@ def test_cascade_decode_rejects_before_launch(pre, code):
     assert _native.lib().pkv_paged_decode_ex(*args) == code
 
 
+def _cascade_args(dec=None, **pre):
+    a = _decode_args(**(dec or {}))[:-1]  # without the stream
+    p = dict(first_block=1 << 12, lse=None, ptab=1 << 12, ptsb=4, pw=4, pctx=1 << 12,
+             pcu=1 << 12, pchunks=1, pmaxq=2, pqrows=1 << 12, pout=1 << 12, plse=1 << 12,
+             prow=1 << 12, parts=1, pstride=2, pwg=0, stream=None)  # fmt: skip
+    p.update(pre)
+    return a + list(p.values())
+
+
+@pytest.mark.parametrize(
+    ("dec", "pre", "code"),
+    [({}, {"pout": None}, -5), ({}, {"plse": None}, -5), ({}, {"prow": None}, -5),
+     ({}, {"parts": 0}, -2), ({}, {"pchunks": -1}, -2), ({}, {"pout": (1 << 12) + 4}, -3),
+     ({"out": (1 << 12) + 2}, {}, -3), ({"out": (1 << 12) + 2}, {"pwg": -1}, -3),
+     ({}, {}, -4), ({"kv_dtype": 7}, {}, -1)],
+)  # fmt: skip
+def test_cascade_one_call_rejects_before_launch(dec, pre, code):
+    """pkv_cascade_decode checks the prefix pass's and the decode pass's arguments on the
+    host before it launches either pass (a 2-sequence batch takes the two-launch form;
+    its decode arguments, here without the workspace a cut needs, are checked before
+    the prefix pass is launched)."""
+    assert _native.lib().pkv_cascade_decode(*_cascade_args(dec, **pre)) == code
+
+
+def test_cascade_one_launch_query():
+    """Shapes without a one-launch form answer 0 on any machine: batches of at most 64
+    sequences, fp32 caches, head_dim 256, blocks that are not a power of two >= 16."""
+    lib = _native.lib()
+    for kv, hd, bs, batch in ((2, 128, 16, 64), (0, 128, 16, 256), (2, 256, 16, 256),
+                              (2, 128, 12, 256), (2, 128, 8, 256), (2, 128, 16, 1025)):
+        assert lib.pkv_cascade_one_launch(kv, hd, 24, 8, bs, batch) == 0
+    assert not pa.cascade_one_launch(torch.bfloat16, 128, 24, 8, 16, 256, torch.device("cpu"))
+
+
 def test_append_and_copy_reject_before_launch():
     lib = _native.lib()
     # bad dtype code

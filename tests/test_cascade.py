@@ -158,6 +158,71 @@ def test_cascade_many_parts_and_pieces(wgs):
     assert (got.cpu() - want).abs().max().item() <= 2e-3
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize(("b", "nh", "nkv", "hd", "bs", "dtype"), [
+    (65, 24, 8, 128, 16, torch.bfloat16),
+    (130, 32, 8, 64, 32, torch.float16),
+    (300, 24, 8, 128, 16, torch.bfloat16),
+    (96, 64, 8, 64, 16, torch.bfloat16),    # 8 heads a group: two rows of tasks (grid y 2)
+    (200, 16, 16, 128, 16, torch.float16),  # 16 KV heads: two rows of tasks
+])  # fmt: skip
+@pytest.mark.parametrize("pwg", [None, 1, 7, 10_000])
+def test_cascade_one_launch_matches_two_launches(b, nh, nkv, hd, bs, dtype, pwg):
+    """Batches of 65-1,024 sequences at head_dim 64/128 run the prefix pass on the first
+    workgroups of the decode pass's launch (they then stream a share of the units); the
+    library's choice of how many (None), one workgroup taking every prefix item in turn,
+    7, and more than the GPU holds (two launches). Five sequences share nothing, tails
+    include empty ones. Same result as the two launches within 1e-3 (the unit ranges are
+    cut elsewhere), the oracle's within 2e-3."""
+    from oracle import oracle
+
+    dev = torch.device("cuda:0")
+    print("[case] one launch", b, nh, nkv, hd, bs, dtype, pwg, flush=True)
+    tables, ctx, nblk = _shared_batch(b=b, shared_blocks=24, bs=bs, extra=5, seed=b)
+    g = torch.Generator().manual_seed(b + 1)
+    k = torch.randn(nblk * bs, nkv, hd, generator=g).to(dtype)
+    v = torch.randn(nblk * bs, nkv, hd, generator=g).to(dtype)
+    q = torch.randn(b, nh, hd, generator=g).to(dtype)
+    assert pa.cascade_one_launch(dtype, hd, nh, nkv, bs, b, dev)
+    pg = pa.find_prefix_groups(tables, ctx, bs, nh, nkv, dev, min_blocks=4, dtype=dtype,
+                               head_dim=hd)  # fmt: skip
+    assert pg is not None and pg.members == b - 5
+    args = (q.to(dev), k.to(dev), v.to(dev), tables.to(dev), ctx.to(dev), bs)
+    one = torch.empty(q.shape, dtype=torch.float32, device=dev)
+    two = torch.empty_like(one)
+    pa.paged_decode_attention(*args, out=one, prefix_groups=pg, prefix_workgroups=pwg)
+    pa.paged_decode_attention(*args, out=two, prefix_groups=pg, prefix_workgroups=-1)
+    torch.cuda.synchronize()
+    want = oracle.decode_attention(q, k, v, tables, ctx, bs, threads=THREADS)
+    assert (one - two).abs().max().item() <= 1e-3
+    assert (one.cpu() - want).abs().max().item() <= 2e-3
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("pieces", [3, 8])
+def test_cascade_one_launch_several_items_per_workgroup(pieces):
+    """More prefix items than prefix workgroups (3 or 8 pieces of a 40-block prefix for
+    256 sequences, 6 row blocks x 8 KV heads each, on 16 prefix workgroups): each
+    workgroup runs items back to back, its rings refilled after every merge."""
+    from oracle import oracle
+
+    dev = torch.device("cuda:0")
+    b, nh, nkv, hd, bs = 256, 24, 8, 128, 16
+    tables, ctx, nblk = _shared_batch(b=b, shared_blocks=40, bs=bs, extra=0, seed=pieces)
+    g = torch.Generator().manual_seed(pieces)
+    k = torch.randn(nblk * bs, nkv, hd, generator=g).to(torch.bfloat16)
+    v = torch.randn(nblk * bs, nkv, hd, generator=g).to(torch.bfloat16)
+    q = torch.randn(b, nh, hd, generator=g).to(torch.bfloat16)
+    pg = pa.find_prefix_groups(tables, ctx, bs, nh, nkv, dev, min_blocks=4, pieces=pieces)
+    assert pg.pieces == pieces
+    args = (q.to(dev), k.to(dev), v.to(dev), tables.to(dev), ctx.to(dev), bs)
+    got = torch.empty(q.shape, dtype=torch.float32, device=dev)
+    pa.paged_decode_attention(*args, out=got, prefix_groups=pg, prefix_workgroups=16)
+    torch.cuda.synchronize()
+    want = oracle.decode_attention(q, k, v, tables, ctx, bs, threads=THREADS)
+    assert (got.cpu() - want).abs().max().item() <= 2e-3
+
+
 def _static_layout(n, pieces, slots, width, tables, ctx, bs, min_blocks, groups=None):
     """The fixed-shape layout a captured decode step reads (stride n, `slots` chunks per
     piece), filled on the host for one step's tables: (flat int32 array, groups used)."""
