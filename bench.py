@@ -42,7 +42,7 @@ sys.path.insert(0, os.path.join(ROOT, "inference-engine_amd"))
 HBM_PEAK_GBPS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_traffic.json")
-DECODE_SOURCES = ("common.h", "decode.hip")  # what the stream pass is compiled from
+DECODE_SOURCES = ("common.h", "decode_kernels.h", "decode.hip")  # what the stream pass is built from
 METRIC = "paged decode attn us/layer-step + achieved HBM GB/s (% of 8 TB/s), 3B shape"
 
 
@@ -346,6 +346,8 @@ def bench_cascade(args, torch, step, pools, out, wgs, unique_bytes) -> dict:
     return {"cascade_us": round(us, 2), "cascade_unique_gbps": round(gbps, 1),
             "cascade_unique_frac": round(gbps / HBM_PEAK_GBPS, 4),
             "cascade_groups": min(len(groups), slots), "cascade_pieces": pieces,
+            "cascade_one_launch": pa.cascade_one_launch(step.k_cache.dtype, step.q.shape[2], nh,
+                                                        nkv, bs, n, step.q.device),
             "cascade_layout": f"decode-graph fixed shape: {slots} group slot(s)"}
 
 
