@@ -417,3 +417,86 @@ def test_decode_refuses_prefix_groups_of_another_step():
     with pytest.raises(ValueError, match="built for"):
         pa.paged_decode_attention(q[:-1], k, k, tables[:-1].to(dev), ctx[:-1].to(dev), 16,
                                   prefix_groups=pg)  # fmt: skip
+
+
+def _groups_batch(r, b, n_groups, bs, tail_max):
+    """b sequences: n_groups groups each sharing its own run of 4-40 leading blocks (two
+    or more members), the rest private; tails of 0..tail_max tokens."""
+    sizes, left = [], b
+    for g in range(n_groups):
+        k = r.randint(2, max(2, left // (n_groups - g) if g < n_groups - 1 else left))
+        k = min(k, left - 2 * (n_groups - g - 1))
+        sizes.append(k)
+        left -= k
+    shared = [r.randint(4, 40) for _ in sizes]
+    tails = [r.choice([0, 1, r.randint(2, tail_max)]) for _ in range(b)]
+    member_of = []
+    for g, k in enumerate(sizes):
+        member_of += [g] * k
+    member_of += [-1] * (b - len(member_of))
+    r.shuffle(member_of)
+    ctx = [(shared[g] * bs if g >= 0 else 0) + t + (1 if g < 0 else 0) for g, t in zip(member_of, tails)]
+    width = max(-(-n // bs) for n in ctx) + 1
+    nblk = sum(shared) + sum(-(-n // bs) for n in ctx) + 4
+    perm = torch.randperm(nblk, generator=torch.Generator().manual_seed(r.randint(0, 1 << 30)))
+    at = 0
+    prefix = []
+    for sh in shared:
+        prefix.append(perm[at : at + sh].int())
+        at += sh
+    tables = torch.zeros(b, width, dtype=torch.int32)
+    for i, (g, n) in enumerate(zip(member_of, ctx)):
+        nb = -(-n // bs)
+        head = 0
+        if g >= 0:
+            tables[i, : shared[g]] = prefix[g]
+            head = shared[g]
+        tables[i, head:nb] = perm[at : at + nb - head].int()
+        at += nb - head
+    return tables, torch.tensor(ctx, dtype=torch.int32), nblk
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(14))
+def test_cascade_random_shapes(seed):
+    """Seeded random cascade steps: 65-600 sequences in 1-3 prefix groups (shared runs of
+    4-40 blocks) plus private sequences, empty and short tails, head_dim 64/128, groups
+    1-8, blocks of 16/32/64 tokens, bf16/fp16, pieces and prefix workgroups drawn or left
+    to the library; one launch where the shapes allow, two launches otherwise. Against
+    the oracle within 2e-3, and against the two-launch form within 1e-3."""
+    import random
+
+    from oracle import oracle
+
+    r = random.Random(4000 + seed)
+    dev = torch.device("cuda:0")
+    hd = r.choice([64, 128])
+    nkv = r.choice([1, 2, 8])
+    groups = r.choice([1, 2, 3, 4, 8])
+    bs = r.choice([16, 32, 64])
+    dtype = r.choice([torch.bfloat16, torch.float16])
+    b = r.choice([65, r.randint(66, 300), r.randint(300, 600)])
+    n_groups = r.choice([1, 1, 2, 3])
+    pieces = r.choice([None, None, 1, 2, 4])
+    pwg = r.choice([None, None, 1, 9, 40])
+    nh = nkv * groups
+    tables, ctx, nblk = _groups_batch(r, b, n_groups, bs, 200)
+    print("[case] cascade random", seed, dict(b=b, hd=hd, nkv=nkv, groups=groups, bs=bs,
+                                              dtype=dtype, n_groups=n_groups, pieces=pieces,
+                                              pwg=pwg), flush=True)  # fmt: skip
+    g = torch.Generator().manual_seed(seed)
+    k = torch.randn(nblk * bs, nkv, hd, generator=g).to(dtype)
+    v = torch.randn(nblk * bs, nkv, hd, generator=g).to(dtype)
+    q = torch.randn(b, nh, hd, generator=g).to(dtype)
+    pg = pa.find_prefix_groups(tables, ctx, bs, nh, nkv, dev, min_blocks=4, pieces=pieces,
+                               dtype=dtype, head_dim=hd)  # fmt: skip
+    assert pg is not None
+    args = (q.to(dev), k.to(dev), v.to(dev), tables.to(dev), ctx.to(dev), bs)
+    one = torch.empty(q.shape, dtype=torch.float32, device=dev)
+    two = torch.empty_like(one)
+    pa.paged_decode_attention(*args, out=one, prefix_groups=pg, prefix_workgroups=pwg)
+    pa.paged_decode_attention(*args, out=two, prefix_groups=pg, prefix_workgroups=-1)
+    torch.cuda.synchronize()
+    want = oracle.decode_attention(q, k, v, tables, ctx, bs, threads=THREADS)
+    assert (one.cpu() - want).abs().max().item() <= 2e-3
+    assert (one - two).abs().max().item() <= 1e-3
