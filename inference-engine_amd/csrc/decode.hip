@@ -443,10 +443,11 @@ int cascade_prefix_wg(int kv_dtype, int head_dim, int num_heads, int num_kv_head
     // The thresholds scale with the workgroups the GPU holds at once (prefix workers
     // are wg x ygrid).
     const int64_t slots = (int64_t)num_workgroups * p.ygrid;
+    const int64_t quarter = slots / 4 > 0 ? slots / 4 : 1;
     int64_t workers = items;
     if (items <= 7 * slots / 32) workers = items + slots / 32;
     else if (items > 5 * slots / 16) {
-      const int64_t rounds = (items + slots / 4 - 1) / (slots / 4);
+      const int64_t rounds = (items + quarter - 1) / quarter;
       workers = (items + rounds - 1) / rounds;
     }
     wg = (workers + p.ygrid - 1) / p.ygrid;

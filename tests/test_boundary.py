@@ -141,6 +141,16 @@ def test_cascade_one_call_rejects_before_launch(dec, pre, code):
     assert _native.lib().pkv_cascade_decode(*_cascade_args(dec, **pre)) == code
 
 
+def test_cascade_one_launch_tiny_split_rejects_before_launch():
+    """A batch the one-launch form takes (100 sequences, 16-bit, head_dim 128) with 1-3
+    workgroups in all: the default choice of prefix workgroups handles the tiny split
+    (no division by zero), and a misaligned output is still refused before any launch."""
+    lib = _native.lib()
+    for wgs in (1, 2, 3):
+        args = _cascade_args({"out": (1 << 12) + 2, "batch": 100, "wgs": wgs})
+        assert lib.pkv_cascade_decode(*args) == -3
+
+
 def test_cascade_one_launch_query():
     """Shapes without a one-launch form answer 0 on any machine: batches of at most 64
     sequences, fp32 caches, head_dim 256, blocks that are not a power of two >= 16."""
