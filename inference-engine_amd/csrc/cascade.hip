@@ -7,7 +7,8 @@
 // it. Run on separate streams, the two grids cannot share a CU (one workgroup of either
 // fills a CU's registers), so the dispatcher's interleaving decides. Here one grid holds
 // both: its first prefix_wg workgroups along x take the prefix items in turn (item
-// w, w + W, ...), the other workgroups are the stream pass's unit ranges, so a few CUs
+// w, w + W, ...) and then stream a smaller share of the units (the weighted split of
+// range_start<true>); the other workgroups are the stream pass's full ranges. A few CUs
 // do the matrix work while the rest stream, and the prefix items can be long (few
 // pieces). The stream pass leaves the sequences with prefix parts to the combine, which
 // runs after this launch as before.
@@ -23,7 +24,8 @@ using namespace pkv;
 // Stream share of a prefix workgroup, in eighths of a stream workgroup's.
 constexpr int kCascadeTailEighths = PKV_CASCADE_TAIL_EIGHTHS;
 
-// Work items of the prefix pass: (chunk, 128-row block, KV head).
+// Work items of the prefix pass: (chunk, row block, KV head); 128-row blocks below
+// head_dim 256, 64-row blocks at 256.
 int64_t prefix_items(const PrefillArgs& p, int64_t rows, int head_dim) {
   const int64_t bm = head_dim >= 256 ? PrefillShape<256>::BM : PrefillShape<128>::BM;
   return (rows + bm - 1) / bm * p.nkv * p.n_chunks;
