@@ -2,8 +2,9 @@
 
     python inference-engine_amd/csrc/build.py
 
-compiles csrc/kv_ops.hip, csrc/decode.hip, csrc/prefill.hip (sharing csrc/common.h) and
-csrc/fused.hip with hipcc for gfx950 into lib/libpaged_kv.so (next to the engine
+compiles csrc/kv_ops.hip, csrc/decode.hip, csrc/prefill.hip, csrc/cascade.hip (sharing
+csrc/common.h and the kernel headers) and csrc/fused.hip with hipcc for gfx950 into
+lib/libpaged_kv.so (next to the engine
 package). The library links libamdhip64.so.7;
 loaded after ``import torch`` it binds to the HIP runtime torch already loaded (same
 SONAME), so torch's streams and device pointers are valid inside it.

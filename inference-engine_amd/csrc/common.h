@@ -1,9 +1,11 @@
 // common.h -- what the gfx950 kernels of the paged-KV hot path share: element types
 // and conversions, 16-byte vector loads and stores, cross-lane reductions (DPP,
 // permlane), the compile-time tuning knobs, and the host-side argument checks. The
-// kernels themselves live in kv_ops.hip (append, block copy, decode slots), decode.hip
-// (split-K paged decode and its combine) and prefill.hip (chunked prefill on the
-// matrix cores); the C ABI is include/paged_kv.h.
+// kernels themselves live in kv_ops.hip (append, block copy, decode slots),
+// decode_kernels.h (split-K paged decode and its combine; launched by decode.hip),
+// prefill_kernels.h (chunked prefill on the matrix cores; launched by prefill.hip),
+// cascade.hip (cascade decode's two passes in one launch) and fused.hip (RMSNorm tail,
+// RoPE, SiLU x up); the C ABI is include/paged_kv.h.
 //
 // Written for CDNA4 wave64: 16-byte global loads, DPP row reductions, v_exp_f32 for
 // the softmax (exp2 with log2(e) folded into the query scale), fp32 accumulation.

@@ -1,5 +1,7 @@
-// decode.hip -- split-K (stream-K) paged decode attention, its combine pass, and cascade
-// decode's tail pass and merge (include/paged_kv.h: pkv_paged_decode*).
+// decode.hip -- host side of paged decode attention (include/paged_kv.h:
+// pkv_paged_decode*, pkv_decode_*): argument checks, the choice of split, the workspace
+// layout and the launches of the stream-K pass, the per-sequence split pass and the
+// combine (kernels in decode_kernels.h).
 
 #include "cascade.h"
 #include "decode_kernels.h"

@@ -1,5 +1,6 @@
-// prefill.hip -- chunked-prefill attention on the matrix cores, also the prefix pass of
-// cascade decode (include/paged_kv.h: pkv_paged_prefill*).
+// prefill.hip -- chunked-prefill attention (include/paged_kv.h: pkv_paged_prefill*): the
+// argument checks and launches of the matrix-core kernel (prefill_kernels.h, also
+// cascade decode's prefix pass), and the VALU kernel for fp32 K/V and head_dim 16.
 
 #include "cascade.h"
 #include "prefill_kernels.h"
