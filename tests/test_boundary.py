@@ -290,3 +290,19 @@ def test_debug_checks_switch():
         assert not _native.debug_checks()
     finally:
         _native.set_debug_checks(prev)
+
+
+@pytest.mark.parametrize("argv,env", [(["--gpus", "2"], {}), (["--gpus", "8"], {}),
+                                      ([], {"WORLD_SIZE": "2"})])  # fmt: skip
+def test_bench_refuses_more_than_one_gpu(argv, env):
+    """bench.py measures one GPU: asked for more (or launched as one rank of several) it
+    exits with status 2 and says so, before it imports torch or touches a device."""
+    import subprocess
+    import sys
+
+    run_env = {**os.environ, **env}
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), *argv],
+                       capture_output=True, text=True, env=run_env, timeout=60)  # fmt: skip
+    assert r.returncode == 2
+    assert "one GPU only" in r.stderr
+    assert r.stdout == ""
