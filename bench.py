@@ -132,9 +132,10 @@ def cpu_baseline(step, budget_s: float) -> dict:
 
 
 def traffic_of(step_name: str) -> tuple[int | None, str]:
-    """HBM bytes per dispatch of the decode stream pass from the committed rocprofv3
-    counter summary, if it was measured on the decode sources built now (their SHA-256
-    is stored with it); otherwise None and why."""
+    """HBM bytes per dispatch of the workload's dominant kernel (the decode stream pass;
+    the matrix-core prefill at config 5) from the committed rocprofv3 counter summary, if
+    it was measured on the sources built now (the SHA-256 of the entry's source files,
+    the decode sources by default, is stored with it); otherwise None and why."""
     import hashlib
 
     if not os.path.exists(TRAFFIC_FILE):
@@ -144,11 +145,11 @@ def traffic_of(step_name: str) -> tuple[int | None, str]:
     if not entry:
         return None, f"no counter profile for {step_name}"
     h = hashlib.sha256()
-    for name in DECODE_SOURCES:
+    for name in entry.get("source_files", DECODE_SOURCES):
         with open(os.path.join(ROOT, "inference-engine_amd", "csrc", name), "rb") as f:
             h.update(f.read())
     if entry.get("sources_sha256") != h.hexdigest():
-        return None, "stale: the counter profile was taken on other decode sources"
+        return None, "stale: the counter profile was taken on other kernel sources"
     return entry["bytes"], f"{entry['source']} (sources {h.hexdigest()[:12]})"
 
 
@@ -484,6 +485,7 @@ def bench_mixed(args, torch) -> dict:
     dec_gbps = d.kv_bytes() / (t_dec * 1e-6) / 1e9
     # append: every new row read once and written once, K and V
     app_bytes = 2 * m.new_k.numel() * m.new_k.element_size() * 2
+    traffic, traffic_source = traffic_of(m.name)
     return {
         "metric": "mixed chunked-prefill layer-step us (config 5)",
         "value": round(step_us, 2),
@@ -506,8 +508,10 @@ def bench_mixed(args, torch) -> dict:
             "peak": MFMA_BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
-            "traffic": None,
+            "traffic": traffic,
         },
+        "traffic_source": traffic_source,
+        "roofline_scope": "pkv_paged_prefill call (matrix-core prefill)",
         "prefill_us": round(t_pre, 2),
         "prefill_gflop": round(flops / 1e9, 2),
         "decode_us": round(t_dec, 2),
