@@ -306,3 +306,43 @@ def test_bench_refuses_more_than_one_gpu(argv, env):
     assert r.returncode == 2
     assert "one GPU only" in r.stderr
     assert r.stdout == ""
+
+
+def _bench():
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("bench_mod", os.path.join(ROOT, "bench.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def test_committed_traffic_profiles_match_the_sources():
+    """Every counter entry the bench can report as roofline.traffic was measured on the
+    kernel sources committed now (a source edit needs a new rocprofv3 FETCH_SIZE /
+    WRITE_SIZE pass), and its byte counts are consistent."""
+    import json
+
+    bench = _bench()
+    entries = json.load(open(bench.TRAFFIC_FILE))
+    assert set(entries) >= {"c1_llama1b_fp16", "c2_llama3b_bf16", "c3_prefix_shared_bf16",
+                            "c4_llama8b_longctx_bf16", "c5_mixed_llama8b_bf16"}  # fmt: skip
+    for name, e in entries.items():
+        assert e["bytes"] == e["read_bytes"] + e["write_bytes"], name
+        assert os.path.exists(os.path.join(ROOT, e["source"])), name
+        got, why = bench.traffic_of(name)
+        assert got == e["bytes"], f"{name}: {why}"
+
+
+def test_stale_traffic_profile_is_not_reported(monkeypatch, tmp_path):
+    import json
+
+    bench = _bench()
+    entries = json.load(open(bench.TRAFFIC_FILE))
+    entries["c2_llama3b_bf16"]["sources_sha256"] = "0" * 64
+    f = tmp_path / "traffic.json"
+    f.write_text(json.dumps(entries))
+    monkeypatch.setattr(bench, "TRAFFIC_FILE", str(f))
+    got, why = bench.traffic_of("c2_llama3b_bf16")
+    assert got is None and "stale" in why
+    assert bench.traffic_of("no_such_workload") == (None, "no counter profile for no_such_workload")
