@@ -351,9 +351,19 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
     if constexpr (POW2) {
       if (fast && (j + 1) * KT <= n) {
         int id[NLD];
+        if (CH == 16 && NLD == 4 && a.bs_shift == 4) {
+          // 16-token blocks at head_dim 128: DMA r covers keys 16 r + 4 wave .. + 3, all
+          // in block r of the tile, so the four ids are the slot's first four entries:
+          // one 16-byte LDS read instead of four reads and their address arithmetic.
+          const int4 v4 = *reinterpret_cast<const int4*>(ids);
+          const int v[4] = {v4.x, v4.y, v4.z, v4.w};
 #pragma unroll
-        for (int r = 0; r < NLD; ++r)  // every id read before the first DMA
-          id[r] = ids[((j * KT + (r * 256 + wave * kWave) / CH) >> a.bs_shift) - b0];
+          for (int r = 0; r < NLD; ++r) id[r] = v[r & 3];
+        } else {
+#pragma unroll
+          for (int r = 0; r < NLD; ++r)  // every id read before the first DMA
+            id[r] = ids[((j * KT + (r * 256 + wave * kWave) / CH) >> a.bs_shift) - b0];
+        }
         const char* base = kv_base[kv] + (uint32_t)(((j * KT) & (a.bs - 1)) * a.kv_ss * (int)sizeof(S));
 #pragma unroll
         for (int r = 0; r < NLD; ++r) {
