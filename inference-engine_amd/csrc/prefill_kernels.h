@@ -88,11 +88,11 @@ template <> struct Mfma16x16x32Bits<PKV_BF16> {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       h[i] = __builtin_bit_cast(uint32_t, v2{(__bf16)p[2 * i], (__bf16)p[2 * i + 1]});
-      // the empty asm keeps h[i] one value (no second conversion to rebuild its low half)
-      uint32_t hv = h[i];
-      __asm__("" : "+v"(hv));
-      const float r0 = p[2 * i] - __uint_as_float(hv << 16);
-      const float r1 = p[2 * i + 1] - __uint_as_float(hv & 0xFFFF0000u);
+      // the empty asm keeps h[i] one value (no second conversion to rebuild its low half);
+      // on h[i] itself, so no copy of it is made
+      __asm__("" : "+v"(h[i]));
+      const float r0 = p[2 * i] - __uint_as_float(h[i] << 16);
+      const float r1 = p[2 * i + 1] - __uint_as_float(h[i] & 0xFFFF0000u);
       l[i] = __builtin_bit_cast(uint32_t, v2{(__bf16)r0, (__bf16)r1});
     }
     hi = u32x4{h[0], h[1], h[2], h[3]};
@@ -166,6 +166,19 @@ __device__ __forceinline__ void mfma_phase_end() {
 #if PKV_PREFILL_SETPRIO
   __builtin_amdgcn_s_setprio(0);
 #endif
+}
+
+// Maximum over lanes l, l^16, l^32, l^48 (the four rows of a column) of scores that are
+// finite or -inf. The swaps return raw bits, which fmaxf would first canonicalise (two
+// extra instructions per step); these values are never signalling NaNs, so v_max_f32
+// takes them as they are.
+__device__ __forceinline__ float score_rows_max(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  float y;
+  __asm__("v_max_f32 %0, %1, %2" : "=v"(y) : "v"(__uint_as_float(a[0])), "v"(__uint_as_float(a[1])));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+  __asm__("v_max_f32 %0, %1, %2" : "=v"(y) : "v"(__uint_as_float(b[0])), "v"(__uint_as_float(b[1])));
+  return y;
 }
 
 template <int HD> struct PrefillShape {
@@ -407,10 +420,12 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
   };
 
   float m_run[RT], l_run[RT];
+  float nref[RT];  // minus the exponent reference: -m_run, or 0 while m_run is -inf
   f32x4 o[RT][DTL];
 #pragma unroll
   for (int t = 0; t < RT; ++t) {
     m_run[t] = -INFINITY;
+    nref[t] = 0.f;
     l_run[t] = 0.f;
 #pragma unroll
     for (int d = 0; d < DTL; ++d) o[t][d] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -546,7 +561,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
       for (int beta = 0; beta < NBETA; ++beta)
 #pragma unroll
         for (int r = 0; r < 4; ++r) x = fmaxf(x, sc[t][beta][r]);
-      mx[t] = rows_max(x) * a.scale_log2;
+      mx[t] = score_rows_max(x) * a.scale_log2;
       raise[t] = mx[t] > m_run[t] + 8.f;  // also true the first time (m_run = -inf)
       any = any || raise[t];
     }
@@ -557,6 +572,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
         // half's tiles can all lie past a row's causal limit).
         const float alpha = raise[t] ? __builtin_amdgcn_exp2f(m_run[t] - mx[t]) : 1.f;
         m_run[t] = raise[t] ? mx[t] : m_run[t];
+        nref[t] = raise[t] ? -mx[t] : nref[t];  // a raise sets a finite maximum
         l_run[t] *= alpha;
 #pragma unroll
         for (int d = 0; d < DTL; ++d) o[t][d] *= alpha;
@@ -564,15 +580,14 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
     }
 #pragma unroll
     for (int t = 0; t < RT; ++t) {
-      const float mref = m_run[t] == -INFINITY ? 0.f : m_run[t];
       float psum = 0.f;
 #pragma unroll
       for (int beta = 0; beta < NBETA; ++beta)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {  // probabilities replace the scores
-          const float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[t][beta][r], a.scale_log2, -mref));
+          const float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[t][beta][r], a.scale_log2, nref[t]));
           sc[t][beta][r] = pr;
-          psum += pr;
+          psum = (beta == 0 && r == 0) ? pr : psum + pr;  // p >= 0: the same sum as 0 + p + ...
         }
       // The first 32-key step's P^T fragments are packed here (hi and lo into score
       // blocks 0 and 1); P.V packs the others, balancing the two phases.
