@@ -324,7 +324,9 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
   const int nlast = max(n - 1, 0);
   auto blk_of = [&](int p) { return POW2 ? (p >> a.bs_shift) : p / a.bs; };
   const int blast = blk_of(nlast);
-  const uint32_t ring_lds = lds_addr(&ring[half][0][0][0]);
+  // This wave's first granule of a stage: the DMA of instruction r then lands at a
+  // compile-time offset r * 4 KiB from it (no per-r register for the wave's part).
+  const uint32_t ring_lds = lds_addr(&ring[half][0][0][0]) + (uint32_t)(wave * kWave * 16);
   const uint32_t ids_lds = lds_addr(&idring[half][0][wave][0]);
   // Local tile m of this half is tile tbeg + m; past the half's end, the last one (the
   // loads keep their count; their stages are free).
@@ -383,7 +385,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
           uint32_t bid = (uint32_t)__builtin_amdgcn_readfirstlane(id[r]);
           bid = bid < pool_blocks ? bid : 0u;  // memory safety only
           dma16_to_lds_s(base + (uint64_t)bid * blk_bytes32, lane_off[r],
-                         dst + (uint32_t)((r * 256 + wave * kWave) * 16));
+                         dst + (uint32_t)(r * 256 * 16));
         }
         return;
       }
@@ -403,7 +405,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
           const int64_t base = (bid * a.bs * a.kv_ss + (int64_t)kvh * a.kv_sh) * (int64_t)sizeof(S);
           const int in_blk = min(seg + lane / CH, nlast) - blk * a.bs;
           const uint32_t lo = (uint32_t)((in_blk * a.kv_ss + chk_of(r) * 8) * (int64_t)sizeof(S));
-          dma16_to_lds(src + base + lo, dst + (uint32_t)((r * 256 + wave * kWave) * 16));
+          dma16_to_lds(src + base + lo, dst + (uint32_t)(r * 256 * 16));
         }
         return;
       }
@@ -415,7 +417,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
       int64_t sl = (int64_t)ids[blk - b0] * a.bs + (p - blk * a.bs);
       sl = (sl >= 0 && sl < a.num_slots) ? sl : 0;
       const int64_t off = (sl * a.kv_ss + (int64_t)kvh * a.kv_sh + chk_of(r) * 8) * (int64_t)sizeof(S);
-      dma16_to_lds(src + off, dst + (uint32_t)((r * 256 + wave * kWave) * 16));
+      dma16_to_lds(src + off, dst + (uint32_t)(r * 256 * 16));
     }
   };
 
