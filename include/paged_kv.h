@@ -226,6 +226,8 @@ int32_t pkv_cascade_one_launch(int kv_dtype, int32_t head_dim, int32_t num_heads
  * prefix_parts, prefix_stride), with the same arguments, results and errors as those two
  * calls. prefix_out (fp32 [rows, num_heads, head_dim], contiguous, 16-byte aligned) and
  * prefix_lse (fp32 [rows, num_heads]) are the caller's scratch for the parts.
+ * An empty prefix layout (prefix_chunks or prefix_max_queries 0) returns PKV_E_SHAPE:
+ * no part would be written for the merge to read.
  * prefix_workgroups < 0 runs the two passes as two launches. Otherwise, for 16-bit K/V at
  * head_dim 64 or 128, power-of-two blocks of at least 16 tokens, 65 to 1,024 sequences and
  * at least 8 (KV head, head sub-group) tasks, the two passes share one launch:

@@ -139,7 +139,10 @@ int pkv_cascade_decode(void* out, int out_dtype, int64_t out_stride_b, int64_t o
                               prefix_chunks, prefix_max_queries, num_heads, num_kv_heads,
                               head_dim, block_size, scale, 0, prefix_q_rows, prefix_lse);
   if (st < 0) return st;
-  const int64_t items = st == 0 ? prefix_items(p, rows, head_dim) : 0;
+  // An empty prefix layout (no chunks or no queries) writes no parts, yet the merge
+  // would read prefix_parts of them for every sequence with a prefix row: refused.
+  if (st == 1) return PKV_E_SHAPE;
+  const int64_t items = prefix_items(p, rows, head_dim);
   const int wg = cascade_prefix_wg(kv_dtype, head_dim, num_heads, num_kv_heads, block_size, batch,
                                    num_workgroups, items, prefix_workgroups);
   if (wg > 0) {
@@ -161,7 +164,7 @@ int pkv_cascade_decode(void* out, int out_dtype, int64_t out_stride_b, int64_t o
                             prefix_out, prefix_lse, prefix_row, prefix_parts, prefix_stride,
                             stream, nullptr, true);
   if (bad) return bad;
-  if (st == 0) {
+  {
     const int e = pkv_paged_prefill_ex(
         prefix_out, PKV_F32, (int64_t)num_heads * head_dim, head_dim, q, q_stride_b, q_stride_h,
         k_cache, v_cache, kv_dtype, kv_stride_slot, kv_stride_head, num_slots, prefix_tables,

@@ -549,12 +549,14 @@ int pkv_paged_decode_noalloc(void* out, int out_dtype, int64_t out_stride_b,
     return PKV_E_SHAPE;
   // The same workspace layout the allocating entry point asks its caller for; it must
   // fit the static array (no contents need clearing: every record is written before
-  // the combine reads it, within the call). The default split (0) is sized for its
-  // stream-K count, an upper bound of what it uses.
+  // the combine reads it, within the call). The default split (0) is sized by what it
+  // runs: the one-launch split pass needs no workspace (and no symbol lookup), stream-K
+  // its workgroup count's records.
   int sized = num_workgroups;
   if (sized == 0 && batch > 0) {
-    sized = pkv_decode_workgroups(kv_dtype, head_dim, num_heads, num_kv_heads);
-    if (sized < 1) return sized < 0 ? sized : PKV_E_HIP;
+    sized = pkv_decode_default_workgroups(kv_dtype, head_dim, num_heads, num_kv_heads, batch,
+                                          max_blocks, block_size);
+    if (sized < 0) return sized;
   }
   const int64_t need = decode_ws(sized, batch, num_heads, head_dim, false).total;
   if (need > PKV_NOALLOC_SCRATCH_BYTES) return PKV_E_SCRATCH;

@@ -202,80 +202,100 @@ class MixedGraphs:
     no tokens. Every op outside attention treats rows independently, so real rows
     compute exactly what they would in an eager step.
 
-    ``max_blocks_per_seq`` (table width of the static buffers) defaults to the pool's
-    block count, which holds any table.
+    Static metadata lives in two device blocks: int64 ``[ids | positions | slots |
+    chunk rows (T each) | last | decode rows (S each)]`` and int32 ``[decode ctx | chunk
+    ctx (S each) | cu_q (S + 1) | decode tables | chunk tables (S x W each)]`` for the
+    largest bucket T, ``max_seqs`` S and table width W. W is ``max_blocks_per_seq`` or,
+    by default, the blocks of the longest sequence the model and pool allow
+    (``model.cfg.max_position_embeddings`` capped by the pool, the bound the reference's
+    engine gives its decode graphs, engine/runtime/engine.py:75-77, :96-99). A step
+    writes only the rows and columns it uses: the kernels never read a table column
+    past a context's last block, so stale entries there are harmless, and a padding
+    decode row reads column 0 only, which is the one column reset when a row turns
+    into padding. A step's cost therefore follows its own size, not W or the pool.
     """
 
     def __init__(self, model: Callable, cache: PagedKVCache, scratch_block: int,
                  max_seqs: int, max_tokens: int,
                  max_blocks_per_seq: int | None = None) -> None:  # fmt: skip
-        self.model, self.cache = model, cache
-        dev = cache.k.device
-        cap = min(max_tokens + 1, TOKEN_BUCKETS[-1])
-        self.sizes = [s for s in TOKEN_BUCKETS if s < cap] + [cap]
-        w = max_blocks_per_seq or cache.num_blocks
-        t, b = self.sizes[-1], max_seqs
-        self.max_seqs, self.max_width = b, w
-        self.scratch_block = scratch_block
+        if max_seqs < 1 or max_tokens < 1:
+            raise ValueError("MixedGraphs: max_seqs and max_tokens must be >= 1")
+        self.model, self.cache, self.scratch_block = model, cache, scratch_block
         self.scratch_slot = scratch_block * cache.block_size
-        i64, i32 = torch.int64, torch.int32
-        self.ids = torch.zeros(1, t, dtype=i64, device=dev)
-        self.pos = torch.zeros(1, t, dtype=i64, device=dev)
-        self.slots = torch.full((t,), self.scratch_slot, dtype=i64, device=dev)
-        self.last = torch.zeros(b, dtype=i64, device=dev)
-        self.dec_rows = torch.zeros(b, dtype=i64, device=dev)
-        self.dec_tables = torch.full((b, w), scratch_block, dtype=i32, device=dev)
-        self.dec_ctx = torch.ones(b, dtype=i32, device=dev)
-        self.ch_rows = torch.zeros(t, dtype=i64, device=dev)
-        self.ch_tables = torch.full((b, w), scratch_block, dtype=i32, device=dev)
-        self.ch_ctx = torch.zeros(b, dtype=i32, device=dev)
-        self.cu_q = torch.zeros(b + 1, dtype=i32, device=dev)
-        self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
-        self.outputs: dict[int, torch.Tensor] = {}
-        self._batches: dict[int, PagedBatch] = {}
-        self._capture()
-
-    def _batch(self, n: int) -> PagedBatch:
-        empty = torch.zeros(0, dtype=torch.int64, device=self.ids.device)
-        return PagedBatch(
-            cache=self.cache, slot_mapping=self.slots[:n], kv_slots=empty, q_index=empty,
-            q_valid=torch.zeros(0, dtype=torch.bool, device=self.ids.device), attn_mask=None,
-            last_index=self.last, use_kernel=False, mixed=True, decode_rows=self.dec_rows,
-            block_tables=self.dec_tables, context_lens=self.dec_ctx, chunks=[],
-            chunk_rows=self.ch_rows[:n], chunk_tables=self.ch_tables, chunk_ctx=self.ch_ctx,
-            cu_seqlens_q=self.cu_q, max_query_len=n)  # fmt: skip
-
-    def _reset(self, n: int) -> None:
-        """Every metadata buffer to its padding value for bucket n (an all-padding step)."""
-        self.ids.zero_()
-        self.pos.zero_()
-        self.slots.fill_(self.scratch_slot)
-        self.last.zero_()
-        self.dec_rows.fill_(n - 1)
-        self.dec_tables.fill_(self.scratch_block)
-        self.dec_ctx.fill_(1)
-        self.ch_rows.fill_(n - 1)
-        self.ch_tables.fill_(self.scratch_block)
-        self.ch_ctx.zero_()
-        self.cu_q.zero_()
-
-    def _capture(self) -> None:
-        pool = None
-        for n in reversed(self.sizes):  # largest first: smaller graphs reuse its pool
-            self._reset(n)
-            batch = self._batch(n)
-            side = torch.cuda.Stream()
-            side.wait_stream(torch.cuda.current_stream())
-            with torch.cuda.stream(side):
-                for _ in range(2):  # warm-up outside the capture
-                    self.model(self.ids[:, :n], self.pos[:, :n], batch)
-            torch.cuda.current_stream().wait_stream(side)
+        top = min(max_tokens + 1, TOKEN_BUCKETS[-1])
+        self.sizes = sorted({s for s in TOKEN_BUCKETS if s < top} | {top})
+        self.max_seqs = max_seqs
+        self.max_width = max_blocks_per_seq or _longest_table(model, cache)
+        big_t, s, w = self.sizes[-1], max_seqs, self.max_width
+        dev = cache.k.device
+        self._i64 = torch.zeros(4 * big_t + 2 * s, dtype=torch.int64, device=dev)
+        ids, pos, self._slots, self._ch_rows, self._last, self._dec_rows = torch.split(
+            self._i64, [big_t, big_t, big_t, big_t, s, s])
+        self._tok = self._i64[: 2 * big_t].view(2, big_t)  # ids and positions, rows 0 / 1
+        self._ids, self._pos = ids.view(1, big_t), pos.view(1, big_t)
+        self._i32 = torch.zeros(3 * s + 1 + 2 * s * w, dtype=torch.int32, device=dev)
+        dctx, cctx, self._cu_q, dtab, ctab = torch.split(
+            self._i32, [s, s, s + 1, s * w, s * w])
+        self._dec_ctx, self._ch_ctx = dctx, cctx
+        self._dec_tab, self._ch_tab = dtab.view(s, w), ctab.view(s, w)
+        # ids and positions go up in one asynchronous copy from pinned memory
+        self._host_tok = torch.zeros(2, big_t, dtype=torch.int64, pin_memory=True)
+        self._sent = torch.cuda.Event()
+        self._sent.record()
+        # what the previous step wrote: (tokens, decode rows, chunks, bucket)
+        self._prev = (big_t, s, s, big_t)
+        self._dec_tab.fill_(scratch_block)
+        self._graphs: dict[int, torch.cuda.CUDAGraph] = {}
+        self._logits: dict[int, torch.Tensor] = {}
+        self._views = {n: self._batch_of(n) for n in self.sizes}
+        self._pad(self.sizes[-1], 0, 0, 0)  # an all-padding step for the warm-up
+        pool = torch.cuda.graph_pool_handle()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):  # warm-up outside any capture: libraries pick kernels
+            for n in self.sizes:
+                self._pad(n, 0, 0, 0)
+                self._forward(n)
+        torch.cuda.current_stream().wait_stream(side)
+        for n in self.sizes:
+            self._pad(n, 0, 0, 0)
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph, pool=pool):
-                out = self.model(self.ids[:, :n], self.pos[:, :n], batch)
-            pool = graph.pool()
-            self.graphs[n], self.outputs[n], self._batches[n] = graph, out, batch
+                self._logits[n] = self._forward(n)
+            self._graphs[n] = graph
         torch.cuda.synchronize()
+
+    def _batch_of(self, n: int) -> PagedBatch:
+        """Bucket n's mixed batch, every tensor a view of the static blocks (the graph
+        reads them by address)."""
+        empty = torch.zeros(0, dtype=torch.int64, device=self._i64.device)
+        return PagedBatch(
+            cache=self.cache, slot_mapping=self._slots[:n], kv_slots=empty, q_index=empty,
+            q_valid=torch.zeros(0, dtype=torch.bool, device=self._i64.device), attn_mask=None,
+            last_index=self._last, use_kernel=False, mixed=True, decode_rows=self._dec_rows,
+            block_tables=self._dec_tab, context_lens=self._dec_ctx, chunks=[],
+            chunk_rows=self._ch_rows[:n], chunk_tables=self._ch_tab, chunk_ctx=self._ch_ctx,
+            cu_seqlens_q=self._cu_q, max_query_len=n)  # fmt: skip
+
+    def _forward(self, n: int) -> torch.Tensor:
+        return self.model(self._ids[:, :n], self._pos[:, :n], self._views[n])
+
+    def _pad(self, n: int, t: int, d: int, c: int, tq: int = 0) -> None:
+        """Padding for bucket n around a step of t tokens, d decode rows, c chunks of tq
+        tokens in all: only what this step leaves unwritten and the previous step (or
+        a smaller bucket) may have left stale."""
+        t_prev, d_prev, _, _ = self._prev
+        self._tok[:, t:n].zero_()
+        self._slots[t:n].fill_(self.scratch_slot)
+        self._last.zero_()  # stale indices could point past this bucket
+        self._dec_rows[d:].fill_(n - 1)
+        self._dec_ctx[d:].fill_(1)
+        if d < d_prev:  # rows that were real and now pad read column 0 only
+            self._dec_tab[d:d_prev, 0].fill_(self.scratch_block)
+        self._ch_rows[tq:n].fill_(n - 1)
+        self._ch_ctx[c:].zero_()
+        self._cu_q[c + 1 :].fill_(tq)  # padding chunks: empty
+        self._prev = (t, d, c, n)
 
     def can_run(self, num_tokens: int, num_seqs: int, width: int | None = None) -> bool:
         return (num_tokens < self.sizes[-1] and num_seqs <= self.max_seqs
@@ -285,25 +305,47 @@ class MixedGraphs:
             batch: PagedBatch) -> torch.Tensor:  # fmt: skip
         """One mixed step: the step's flattened token ids and positions and its mixed
         ``PagedBatch`` (built as for an eager step) -> logits [B, 1, vocab]."""
-        t, b = len(ids), batch.last_index.numel()
-        n = next(s for s in self.sizes if s > t)
-        self._reset(n)
-        self.ids[0, :t].copy_(torch.tensor(list(ids)), non_blocking=True)
-        self.pos[0, :t].copy_(torch.tensor(list(positions)), non_blocking=True)
-        self.slots[:t].copy_(batch.slot_mapping)
-        self.last[:b].copy_(batch.last_index)
-        if batch.block_tables is not None:
-            d, w = batch.block_tables.shape
-            self.dec_rows[:d].copy_(batch.decode_rows)
-            self.dec_tables[:d, :w].copy_(batch.block_tables)
-            self.dec_ctx[:d].copy_(batch.context_lens)
-        if batch.chunk_rows is not None:
-            tq = batch.chunk_rows.numel()
-            c, w = batch.chunk_tables.shape
-            self.ch_rows[:tq].copy_(batch.chunk_rows)
-            self.ch_tables[:c, :w].copy_(batch.chunk_tables)
-            self.ch_ctx[:c].copy_(batch.chunk_ctx)
-            self.cu_q[: c + 1].copy_(batch.cu_seqlens_q)
-            self.cu_q[c + 1 :].fill_(tq)  # padding chunks: empty
-        self.graphs[n].replay()
-        return self.outputs[n][:b]
+        t = len(ids)
+        if not 1 <= t < self.sizes[-1]:
+            raise ValueError(f"MixedGraphs: {t} tokens outside 1..{self.sizes[-1] - 1}")
+        n = self.sizes[bisect.bisect_right(self.sizes, t)]
+        d = 0 if batch.block_tables is None else batch.block_tables.shape[0]
+        c = 0 if batch.chunk_rows is None else batch.chunk_tables.shape[0]
+        tq = 0 if batch.chunk_rows is None else batch.chunk_rows.numel()
+        for rows, width in ((d, None if d == 0 else batch.block_tables.shape[1]),
+                            (c, None if c == 0 else batch.chunk_tables.shape[1])):
+            if rows > self.max_seqs or (width is not None and width > self.max_width):
+                raise ValueError(f"MixedGraphs: {rows} rows of width {width} exceed "
+                                 f"{self.max_seqs} x {self.max_width}")  # fmt: skip
+        self._sent.synchronize()  # the previous step's copy has left the host block
+        h = self._host_tok.numpy()
+        h[0, :t] = ids
+        h[1, :t] = positions
+        self._tok[:, :t].copy_(self._host_tok[:, :t], non_blocking=True)
+        self._sent.record()
+        self._pad(n, t, d, c, tq)
+        self._slots[:t].copy_(batch.slot_mapping)
+        self._last[: batch.last_index.numel()].copy_(batch.last_index)
+        if d:
+            w = batch.block_tables.shape[1]
+            self._dec_rows[:d].copy_(batch.decode_rows)
+            self._dec_tab[:d, :w].copy_(batch.block_tables)
+            self._dec_ctx[:d].copy_(batch.context_lens)
+        if c:
+            w = batch.chunk_tables.shape[1]
+            self._ch_rows[:tq].copy_(batch.chunk_rows)
+            self._ch_tab[:c, :w].copy_(batch.chunk_tables)
+            self._ch_ctx[:c].copy_(batch.chunk_ctx)
+            self._cu_q[: c + 1].copy_(batch.cu_seqlens_q)
+        self._graphs[n].replay()
+        return self._logits[n][: batch.last_index.numel()]
+
+
+def _longest_table(model: Callable, cache: PagedKVCache) -> int:
+    """Blocks of the longest sequence: the model's position limit capped by the pool
+    (less the scratch block), as the reference's engine bounds max_model_len."""
+    bs = cache.block_size
+    pool_tokens = max(cache.num_blocks - 1, 1) * bs
+    limit = getattr(getattr(model, "cfg", None), "max_position_embeddings", None)
+    tokens = min(limit, pool_tokens) if limit else pool_tokens
+    return -(-tokens // bs)

@@ -392,3 +392,12 @@ class PagedBatch:
             batch.cu_seqlens_q = cu.to(device)
             batch.max_query_len = max(ch_q)
         return batch
+
+
+def varlen_available(t: torch.Tensor) -> bool:
+    """Whether mixed steps would gather for FlashAttention's varlen kernel
+    (reference engine/runtime/paged_cache.py:232-240, which its tests call and
+    monkeypatch). Never here: the chunked-prefill kernel reads the paged pool in place, so
+    ``PagedBatch.varlen`` stays None for every device, dtype and torch version."""
+    del t
+    return False

@@ -130,6 +130,7 @@ def _cascade_args(dec=None, **pre):
     ("dec", "pre", "code"),
     [({}, {"pout": None}, -5), ({}, {"plse": None}, -5), ({}, {"prow": None}, -5),
      ({}, {"parts": 0}, -2), ({}, {"pchunks": -1}, -2), ({}, {"pout": (1 << 12) + 4}, -3),
+     ({}, {"pchunks": 0}, -2), ({}, {"pmaxq": 0}, -2),
      ({"out": (1 << 12) + 2}, {}, -3), ({"out": (1 << 12) + 2}, {"pwg": -1}, -3),
      ({}, {}, -4), ({"kv_dtype": 7}, {}, -1)],
 )  # fmt: skip
@@ -137,7 +138,8 @@ def test_cascade_one_call_rejects_before_launch(dec, pre, code):
     """pkv_cascade_decode checks the prefix pass's and the decode pass's arguments on the
     host before it launches either pass (a 2-sequence batch takes the two-launch form;
     its decode arguments, here without the workspace a cut needs, are checked before
-    the prefix pass is launched)."""
+    the prefix pass is launched). An empty prefix layout (no chunks or no queries) with
+    prefix parts to merge is refused: nothing would write the parts the merge reads."""
     assert _native.lib().pkv_cascade_decode(*_cascade_args(dec, **pre)) == code
 
 
@@ -188,6 +190,22 @@ def test_python_signatures_mirror_reference():
     assert pa.use_gqa_kernel(torch.bfloat16, 4, 64)
     assert not pa.use_gqa_kernel(torch.float32, 4, 64)
     assert not pa.use_gqa_kernel(torch.bfloat16, 4, 48)
+
+
+def test_varlen_available_keeps_the_reference_surface(monkeypatch):
+    """The reference exports varlen_available (engine/runtime/paged_cache.py:232-240) and
+    its tests call and monkeypatch it (tests/test_kernels.py:191, :211). Here it exists,
+    takes one tensor, and is False for every device and dtype: mixed steps never gather
+    for varlen, whatever it returns."""
+    assert list(inspect.signature(paged_cache.varlen_available).parameters) == ["t"]
+    for dt in (torch.float32, torch.float16, torch.bfloat16):
+        assert paged_cache.varlen_available(torch.zeros(2, dtype=dt)) is False
+    monkeypatch.setattr(paged_cache, "varlen_available", lambda t: True)
+    cfg = paged_cache.KVShape(2, 2, 16)
+    cache = paged_cache.PagedKVCache(cfg, 8, 4, device="cpu")
+    batch = paged_cache.PagedBatch.build(cache, [[0, 1], [2]], [6, 1], [3, 1], "cpu",
+                                         use_kernel=True)  # fmt: skip
+    assert batch.mixed and batch.varlen is None and batch.chunks == []
 
 
 def test_cpu_tensors_fail_loudly():

@@ -383,6 +383,46 @@ def test_mixed_graphs_match_eager(dtype, budget):
 
 
 @pytest.mark.gpu
+def test_mixed_graphs_step_cost_follows_the_step_not_the_pool():
+    """MixedGraphs built with the reference's five arguments (engine/runtime/engine.py:
+    110-112) sizes its tables by the model's longest sequence, not by the pool, and a
+    step writes only what it uses: pools of 2,000 and 40,000 blocks give the same static
+    buffers, the same logits and the same run() time (within noise)."""
+    import time
+
+    from engine.runtime.cuda_graphs import MixedGraphs
+    from tiny_llama import KernelBackend
+
+    model = _cuda_model(torch.bfloat16)
+    model.attend = KernelBackend().attend
+    tables, ctx, qlens = [[0, 1, 2], [3, 4], [5, 6]], [9, 6, 5], [1, 1, 5]
+    ids = [11, 12, 20, 21, 22, 23, 24]
+    positions = [8, 5, 0, 1, 2, 3, 4]
+    times, logits, sizes = {}, {}, {}
+    for blocks in (2_000, 40_000):
+        cache = PagedKVCache(model.cfg, blocks + 1, 4, "cuda", torch.bfloat16)
+        graphs = MixedGraphs(model, cache, blocks, 64, 64)
+        assert graphs.max_width == model.cfg.max_position_embeddings // 4
+        sizes[blocks] = (graphs._i32.numel(), graphs._i64.numel())
+        batch = PagedBatch.build(cache, tables, ctx, qlens, "cuda", use_kernel=True,
+                                 force_mixed=True)  # fmt: skip
+        for _ in range(3):
+            graphs.run(ids, positions, batch)
+        torch.cuda.synchronize()
+        best = float("inf")
+        for _ in range(5):  # best of 5 rounds of 20 steps
+            t0 = time.perf_counter()
+            for _ in range(20):
+                out = graphs.run(ids, positions, batch)
+            torch.cuda.synchronize()
+            best = min(best, (time.perf_counter() - t0) / 20)
+        times[blocks], logits[blocks] = best, out.clone()
+    assert sizes[2_000] == sizes[40_000]
+    assert torch.equal(logits[2_000], logits[40_000])
+    assert times[40_000] <= 1.3 * times[2_000] + 50e-6, times
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_fused_elementwise_kernels_change_nothing(dtype):
     """RMSNorm, RoPE and SiLU x up on the fused HIP kernels: every logit of every step is

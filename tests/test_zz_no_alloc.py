@@ -44,19 +44,30 @@ def test_noalloc_decode_matches_allocating_entry_point():
         ("config2 full", workloads.config2(DEV, seed=0), None),
         ("smaller: 5 sequences, hd 64, 8 heads", workloads.custom(
             [1, 40, 300, 17, 999], 8, 2, 64, 16, torch.bfloat16, DEV, seed=1), 37),
+        # the library's default split at a small batch: the one-launch split pass, which
+        # needs no scratch (the array is neither sized nor looked up for it)
+        ("default split: config1", workloads.config1(DEV, seed=2), 0),
+        ("default split: 3 sequences, hd 128", workloads.custom(
+            [5, 200, 64], 24, 8, 128, 16, torch.bfloat16, DEV, seed=3), 0),
     ]  # fmt: skip
     for name, step, wgs in steps:
         _say("noalloc", name, "workgroups", wgs)
         args = (step.q, step.k_cache, step.v_cache, step.block_tables, step.context_lens,
                 step.block_size)  # fmt: skip
         b, nh, hd = step.q.shape
-        n_wg = wgs or pa.decode_workgroups(DEV, step.q.dtype, hd, nh, step.k_cache.shape[1])
+        if wgs == 0:  # the default on both entry points
+            n_wg = None
+            assert _native.lib().pkv_decode_default_workgroups(
+                _native.dtype_code(step.k_cache.dtype, "t"), hd, nh, step.k_cache.shape[1], b,
+                step.block_tables.shape[1], step.block_size) == 0, name  # fmt: skip
+        else:
+            n_wg = wgs or pa.decode_workgroups(DEV, step.q.dtype, hd, nh, step.k_cache.shape[1])
         want32 = torch.empty(step.q.shape, dtype=torch.float32, device=DEV)
         pa.paged_decode_attention(*args, out=want32, num_workgroups=n_wg)
         got32 = torch.full_like(want32, float("nan"))
         pa.paged_decode_attention_noalloc(*args, out=got32, num_workgroups=n_wg)
         gotq = torch.empty_like(step.q)
-        _native.check(_direct_noalloc(step, gotq, n_wg), "noalloc direct")
+        _native.check(_direct_noalloc(step, gotq, n_wg or 0), "noalloc direct")
         torch.cuda.synchronize()
         assert torch.equal(got32, want32), name
         assert torch.equal(gotq, want32.to(step.q.dtype)), name

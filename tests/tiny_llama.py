@@ -42,6 +42,7 @@ class TinyConfig:
     num_key_value_heads: int = 2
     rms_norm_eps: float = 1e-5
     rope_theta: float = 10000.0
+    max_position_embeddings: int = 4096
 
     @property
     def head_dim(self) -> int:
