@@ -32,6 +32,27 @@ struct PrefillArgs {
 
 }  // namespace pkv
 
+// Tuning knobs of the matrix-core prefill (compile-time; the defaults are the measured
+// best on MI355X).
+// Matrix phase: operand fragments read this many fragment steps ahead of their MFMAs.
+#ifndef PKV_PREFILL_PIPE
+#define PKV_PREFILL_PIPE 2
+#endif
+// The softmax packs every 32-key step's P fragments (1) or only the first (0; the matrix
+// phase packs the others).
+#ifndef PKV_PREFILL_PACK_ALL
+#define PKV_PREFILL_PACK_ALL 1
+#endif
+// P's lo half (bf16 caches) from v_dot2c_f32_bf16 (1) or unpack-and-subtract (0).
+#ifndef PKV_PREFILL_DOT2LO
+#define PKV_PREFILL_DOT2LO 0
+#endif
+// Wave priority (s_setprio): 1 raises the softmax phase's, 2 raises half 1's waves'
+// (younger, so otherwise second in issue arbitration), 0 leaves both at 0.
+#ifndef PKV_PREFILL_VALU_PRIO
+#define PKV_PREFILL_VALU_PRIO 0
+#endif
+
 namespace {
 
 using namespace pkv;
@@ -77,14 +98,33 @@ template <> struct Mfma16x16x32Bits<PKV_BF16> {
   // bf16 keeps 8 significant bits, too few for softmax weights at a 2e-3 output bar, so
   // P enters the product as hi = bf16(P) plus lo = bf16(P - hi) (two MFMAs).
   static constexpr bool kSplit = true;
+  static constexpr uint32_t kOnePair = 0x3F803F80u;  // two bf16 1.0
   __device__ static f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8, a),
                                                    __builtin_bit_cast(v8, b), c, 0, 0, 0);
   }
   // 8 finite fp32 -> hi and lo operand fragments (v_cvt_pk_bf16_f32, round to nearest
-  // even).
+  // even); lo = p - hi is exact.
   __device__ static void pack8(const float* p, u32x4& hi, u32x4& lo) {
     uint32_t h[4], l[4];
+#if PKV_PREFILL_DOT2LO
+    // lo from one v_dot2c_f32_bf16 per value (p + hi_pair . (-1, 0)). The pairs (-1, 0)
+    // and (0, -1) go in as registers with these exact bits: left to itself the compiler
+    // encodes the first as the inline constant -1.0, whose 32-bit pattern is the second
+    // pair (lo of p0 then came out as p0 - hi of p1). Measured slower than the two plain
+    // instructions per value below (the dot product issues at a lower rate).
+    uint32_t neg_lo = 0x0000BF80u, neg_hi = 0xBF800000u;
+    __asm__("" : "+v"(neg_lo), "+v"(neg_hi));
+    const v2 c0 = __builtin_bit_cast(v2, neg_lo), c1 = __builtin_bit_cast(v2, neg_hi);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const v2 hp = v2{(__bf16)p[2 * i], (__bf16)p[2 * i + 1]};
+      h[i] = __builtin_bit_cast(uint32_t, hp);
+      const float r0 = __builtin_amdgcn_fdot2_f32_bf16(hp, c0, p[2 * i], false);
+      const float r1 = __builtin_amdgcn_fdot2_f32_bf16(hp, c1, p[2 * i + 1], false);
+      l[i] = __builtin_bit_cast(uint32_t, v2{(__bf16)r0, (__bf16)r1});
+    }
+#else
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       h[i] = __builtin_bit_cast(uint32_t, v2{(__bf16)p[2 * i], (__bf16)p[2 * i + 1]});
@@ -95,6 +135,7 @@ template <> struct Mfma16x16x32Bits<PKV_BF16> {
       const float r1 = p[2 * i + 1] - __uint_as_float(h[i] & 0xFFFF0000u);
       l[i] = __builtin_bit_cast(uint32_t, v2{(__bf16)r0, (__bf16)r1});
     }
+#endif
     hi = u32x4{h[0], h[1], h[2], h[3]};
     lo = u32x4{l[0], l[1], l[2], l[3]};
   }
@@ -103,6 +144,7 @@ template <> struct Mfma16x16x32Bits<PKV_F16> {
   typedef _Float16 v8 __attribute__((ext_vector_type(8)));
   typedef _Float16 v2 __attribute__((ext_vector_type(2)));
   static constexpr bool kSplit = false;  // fp16 keeps 11 bits: P rounded once
+  static constexpr uint32_t kOnePair = 0x3C003C00u;  // two fp16 1.0
   __device__ static f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8, a),
                                                   __builtin_bit_cast(v8, b), c, 0, 0, 0);
@@ -331,15 +373,28 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
   // Local tile m of this half is tile tbeg + m; past the half's end, the last one (the
   // loads keep their count; their stages are free).
   auto gtile = [&](int m) { return tbeg + min(m, nt - 1); };
+  // One DMA instruction of one wave covers SEG consecutive keys of a tile. When the block
+  // size is a power of two >= SEG those keys share one block: its id is wave-uniform and
+  // the address is scalar math plus one per-lane offset. The ids then come straight from
+  // the table through the scalar cache (s_load, counted in lgkmcnt), not through the LDS
+  // ring, whose reads queue behind the matrix waves' operand reads (~1,200 cycles of the
+  // VALU phase went to issuing the DMAs that way).
+  constexpr int SEG = kWave / CH;
+  const bool seg_uniform = POW2 && a.bs >= SEG;
+  const uint64_t trow_u = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)trow)) |
+                          ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)((uintptr_t)trow >> 32)) << 32);
+  typedef __attribute__((address_space(4))) const int32_t c_i32;
+  typedef int32_t i32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+  typedef __attribute__((address_space(4))) const i32x4_a4 c_i32x4;
+  auto sid = [&](int b) { return *(c_i32*)(uintptr_t)(trow_u + 4ull * (uint32_t)b); };
+  auto sid4 = [&](int b) { return *(c_i32x4*)(uintptr_t)(trow_u + 4ull * (uint32_t)b); };
+  // The LDS ring of block ids (other block sizes): the 64 entries from tile m's first
+  // block on, two tiles ahead of the K/V loads that read them.
   auto issue_ids = [&](int m) __attribute__((always_inline)) {
+    if (seg_uniform) return;
     const int b = min(blk_of(gtile(m) * KT) + lane, blast);
     dma4_to_lds(trow + b, ids_lds + (uint32_t)((m % 3) * 4 * kWave * 4));
   };
-  // One DMA instruction of one wave covers SEG consecutive keys of a tile. When the block
-  // size is a power of two >= SEG those keys share one block: its id is wave-uniform and
-  // the address is scalar math plus one per-lane offset.
-  constexpr int SEG = kWave / CH;
-  const bool seg_uniform = POW2 && a.bs >= SEG;
   // Fast path (power-of-two blocks of at least SEG keys, tile inside the context): the
   // lane's byte offset inside its block is the same for every tile, plus a uniform part
   // when blocks are longer than a tile.
@@ -368,16 +423,15 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
         int id[NLD];
         if (CH == 16 && NLD == 4 && a.bs_shift == 4) {
           // 16-token blocks at head_dim 128: DMA r covers keys 16 r + 4 wave .. + 3, all
-          // in block r of the tile, so the four ids are the slot's first four entries:
-          // one 16-byte LDS read instead of four reads and their address arithmetic.
-          const int4 v4 = *reinterpret_cast<const int4*>(ids);
-          const int v[4] = {v4.x, v4.y, v4.z, v4.w};
+          // in block r of the tile, so the four ids are the table's entries b0 .. b0 + 3:
+          // one 16-byte scalar load (inside the table: the tile is inside the context).
+          const i32x4_a4 v4 = sid4(b0);
 #pragma unroll
-          for (int r = 0; r < NLD; ++r) id[r] = v[r & 3];
+          for (int r = 0; r < NLD; ++r) id[r] = v4[r & 3];
         } else {
 #pragma unroll
           for (int r = 0; r < NLD; ++r)  // every id read before the first DMA
-            id[r] = ids[((j * KT + (r * 256 + wave * kWave) / CH) >> a.bs_shift) - b0];
+            id[r] = sid((j * KT + (r * 256 + wave * kWave) / CH) >> a.bs_shift);
         }
         const char* base = kv_base[kv] + (uint32_t)(((j * KT) & (a.bs - 1)) * a.kv_ss * (int)sizeof(S));
 #pragma unroll
@@ -394,7 +448,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
 #pragma unroll
         for (int r = 0; r < NLD; ++r) {  // every id read before the first DMA
           const int seg = j * KT + (r * 256 + wave * kWave) / CH;  // first key, uniform
-          id[r] = ids[min(seg >> a.bs_shift, blast) - b0];
+          id[r] = sid(min(seg >> a.bs_shift, blast));
         }
 #pragma unroll
         for (int r = 0; r < NLD; ++r) {
@@ -421,16 +475,19 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
     }
   };
 
-  float m_run[RT], l_run[RT];
+  float m_run[RT];
   float nref[RT];  // minus the exponent reference: -m_run, or 0 while m_run is -inf
-  f32x4 o[RT][DTL];
+  // O^T tiles d < DTL; tile DTL is the softmax normaliser: the matrix cores multiply each
+  // P^T fragment by an all-ones V^T fragment too, so every lane of row n's column holds
+  // row n's sum of the same (hi + lo) weights O carries -- no VALU adds, no cross-lane sum.
+  f32x4 o[RT][DTL + 1];
+  const u32x4 ones = {MMA::kOnePair, MMA::kOnePair, MMA::kOnePair, MMA::kOnePair};
 #pragma unroll
   for (int t = 0; t < RT; ++t) {
     m_run[t] = -INFINITY;
     nref[t] = 0.f;
-    l_run[t] = 0.f;
 #pragma unroll
-    for (int d = 0; d < DTL; ++d) o[t][d] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int d = 0; d <= DTL; ++d) o[t][d] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
   // Rows whose causal limit a tile can cross: tile j needs the mask only if it reaches
@@ -468,6 +525,8 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
   // probabilities P^T until its P.V (the first 32-key step's already packed as operand
   // fragments: hi in block 0, lo in block 1).
   static_assert(NBETA == 2 * NSG, "two score blocks per P^T fragment pair");
+  // 32-key steps whose P^T fragments the softmax packs (the rest: the matrix phase)
+  constexpr int kPackedSteps = PKV_PREFILL_PACK_ALL ? NSG : 1;
   f32x4 sc[RT][NBETA];
 
   // S^T = K . Q^T of local tile m: block beta holds keys 16 beta + 4 grp + r for query
@@ -505,9 +564,9 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
       u32x4 phi[RT], plo[RT];
 #pragma unroll
       for (int t = 0; t < RT; ++t) {
-        if (sg == 0) {
-          phi[t] = __builtin_bit_cast(u32x4, sc[t][0]);
-          plo[t] = __builtin_bit_cast(u32x4, sc[t][1]);
+        if (sg < kPackedSteps) {
+          phi[t] = __builtin_bit_cast(u32x4, sc[t][2 * sg]);
+          plo[t] = __builtin_bit_cast(u32x4, sc[t][2 * sg + 1]);
         } else {
           float p8[8];
 #pragma unroll
@@ -533,6 +592,93 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
           if constexpr (MMA::kSplit) o[t][d] = MMA::mma(vf, plo[t], o[t][d]);
         }
       }
+#pragma unroll
+      for (int t = 0; t < RT; ++t) {  // the row sums
+        o[t][DTL] = MMA::mma(ones, phi[t], o[t][DTL]);
+        if constexpr (MMA::kSplit) o[t][DTL] = MMA::mma(ones, plo[t], o[t][DTL]);
+      }
+    }
+  };
+  // The steady-state matrix phase: P.V of local tile mp, then QK^T of tile mq, as one
+  // software pipeline over their NV + NK operand fragments: step i issues the LDS reads of
+  // fragment i + PIPE, then the MFMAs of fragment i, and a scheduling fence closes each
+  // step. Left to itself the compiler moves every read down to just before its own MFMAs,
+  // so each group of MFMAs waits out a whole LDS round trip: a timing kernel of this phase
+  // (4 waves of 96 MFMAs on LDS fragments, 256 CUs) took 2,000 cycles that way and 1,520
+  // (its MFMA time) with the reads two fragments ahead. Same products, same order of
+  // accumulation as pv then qk.
+  constexpr int PIPE = PKV_PREFILL_PIPE > 0 ? PKV_PREFILL_PIPE : 1;
+  constexpr int NV = NSG * DTL, NK = NBETA * KS;
+  auto pv_qk = [&](int mp, int mq) __attribute__((always_inline)) {
+    const char* vstage = reinterpret_cast<const char*>(&ring[half][1][mp & 1][0]);
+    const char* kstage = reinterpret_cast<const char*>(&ring[half][0][mq & 1][0]);
+    const int l = fresh_lane();
+    u32x4 phi[NSG][RT], plo[NSG][RT];
+#pragma unroll
+    for (int sg = 0; sg < kPackedSteps; ++sg)
+#pragma unroll
+      for (int t = 0; t < RT; ++t) {
+        phi[sg][t] = __builtin_bit_cast(u32x4, sc[t][2 * sg]);
+        plo[sg][t] = __builtin_bit_cast(u32x4, sc[t][2 * sg + 1]);
+      }
+#pragma unroll
+    for (int sg = kPackedSteps; sg < NSG; ++sg)
+#pragma unroll
+      for (int t = 0; t < RT; ++t) {
+        float p8[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) p8[e] = sc[t][2 * sg + e / 4][e % 4];
+        MMA::pack8(p8, phi[sg][t], plo[sg][t]);
+      }
+    // fragment i: V^T (sg, d) = (i / DTL, i % DTL) for i < NV, else K (beta, s)
+    auto read_frag = [&](int i) __attribute__((always_inline)) {
+      u32x4 f;
+      if (i < NV) {
+        const int sg = i / DTL, d = i % DTL;
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+          const s16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_s16x4*)(vstage + (32 * sg + 16 * h2) * CH * 16 + voff(l, VSW == 1 ? 0 : h2, d)));
+          const uint32_t lo = (uint32_t)(uint16_t)x[0] | ((uint32_t)(uint16_t)x[1] << 16);
+          const uint32_t hi = (uint32_t)(uint16_t)x[2] | ((uint32_t)(uint16_t)x[3] << 16);
+          if (h2 == 0) { f.x = lo; f.y = hi; } else { f.z = lo; f.w = hi; }
+        }
+      } else {
+        const int beta = (i - NV) / KS, s = (i - NV) % KS;
+        f = *reinterpret_cast<const u32x4*>(kstage + beta * 16 * CH * 16 +
+                                            koff(l, KSW == 1 ? 0 : beta, s));
+      }
+      return f;
+    };
+    auto mma_frag = [&](int i, const u32x4& f) __attribute__((always_inline)) {
+      if (i < NV) {
+        const int sg = i / DTL, d = i % DTL;
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+          o[t][d] = MMA::mma(f, phi[sg][t], o[t][d]);
+          if constexpr (MMA::kSplit) o[t][d] = MMA::mma(f, plo[sg][t], o[t][d]);
+        }
+        if (d == DTL - 1)
+#pragma unroll
+          for (int t = 0; t < RT; ++t) {  // the row sums
+            o[t][DTL] = MMA::mma(ones, phi[sg][t], o[t][DTL]);
+            if constexpr (MMA::kSplit) o[t][DTL] = MMA::mma(ones, plo[sg][t], o[t][DTL]);
+          }
+      } else {
+        const int beta = (i - NV) / KS, s = (i - NV) % KS;
+#pragma unroll
+        for (int t = 0; t < RT; ++t)
+          sc[t][beta] = MMA::mma(f, qf[t][s], s == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : sc[t][beta]);
+      }
+    };
+    u32x4 buf[PIPE + 1];
+#pragma unroll
+    for (int i = 0; i < PIPE; ++i) buf[i] = read_frag(i);
+#pragma unroll
+    for (int i = 0; i < NV + NK; ++i) {
+      if (i + PIPE < NV + NK) buf[(i + PIPE) % (PIPE + 1)] = read_frag(i + PIPE);
+      mma_frag(i, buf[i % (PIPE + 1)]);
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
   // Online softmax of global tile j's scores into P^T fragments; masked: some key of the
@@ -575,34 +721,29 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
         const float alpha = raise[t] ? __builtin_amdgcn_exp2f(m_run[t] - mx[t]) : 1.f;
         m_run[t] = raise[t] ? mx[t] : m_run[t];
         nref[t] = raise[t] ? -mx[t] : nref[t];  // a raise sets a finite maximum
-        l_run[t] *= alpha;
 #pragma unroll
-        for (int d = 0; d < DTL; ++d) o[t][d] *= alpha;
+        for (int d = 0; d <= DTL; ++d) o[t][d] *= alpha;
       }
     }
 #pragma unroll
     for (int t = 0; t < RT; ++t) {
-      float psum = 0.f;
 #pragma unroll
       for (int beta = 0; beta < NBETA; ++beta)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {  // probabilities replace the scores
-          const float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[t][beta][r], a.scale_log2, nref[t]));
-          sc[t][beta][r] = pr;
-          psum = (beta == 0 && r == 0) ? pr : psum + pr;  // p >= 0: the same sum as 0 + p + ...
-        }
-      // The first 32-key step's P^T fragments are packed here (hi and lo into score
-      // blocks 0 and 1); P.V packs the others, balancing the two phases.
-      {
+        for (int r = 0; r < 4; ++r)  // probabilities replace the scores
+          sc[t][beta][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[t][beta][r], a.scale_log2, nref[t]));
+      // The P^T fragments of the first kPackedSteps 32-key steps are packed here (hi and
+      // lo of step sg into score blocks 2 sg and 2 sg + 1); P.V packs the others.
+#pragma unroll
+      for (int sg = 0; sg < kPackedSteps; ++sg) {
         float p8[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) p8[e] = sc[t][e / 4][e % 4];
+        for (int e = 0; e < 8; ++e) p8[e] = sc[t][2 * sg + e / 4][e % 4];
         u32x4 hi, lo;
         MMA::pack8(p8, hi, lo);
-        sc[t][0] = __builtin_bit_cast(f32x4, hi);
-        sc[t][1] = __builtin_bit_cast(f32x4, lo);
+        sc[t][2 * sg] = __builtin_bit_cast(f32x4, hi);
+        sc[t][2 * sg + 1] = __builtin_bit_cast(f32x4, lo);
       }
-      l_run[t] += psum;
     }
   };
 
@@ -618,53 +759,78 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
   // all but that phase's K and V loads (its block ids must be in). Loads complete in
   // issue order.
   if (nt > 0) {  // prologue: block ids of tiles 0-2, K of 0 and 1, V of 0
-    issue_ids(0);
-    issue_ids(1);
-    wait_vmcnt<0>();
+    if (!seg_uniform) {  // the LDS ring's ids must land first; scalar-loaded ids need not
+      issue_ids(0);      // wait for the query loads still in flight
+      issue_ids(1);
+      wait_vmcnt<0>();
+    }
     issue_tile(0, 0);
     issue_ids(2);
     issue_tile(0, 1);
     issue_tile(1, 0);
     wait_vmcnt<0>();
   }
-  // Matrix phase of iteration m and VALU phase of iteration m, each closed by its
+  // Matrix phase of iteration m and VALU phase of iteration m, each opened by its
   // barrier. Half 0 runs intervals (M0 V0)(M1 V1)..(M_ns V_ns); half 1 one interval
-  // later: idle, (M0 V0)..(M_ns-1 V_ns-1) M_ns. Both pass 2 ns + 2 barriers.
-  auto interval_m = [&](int m) __attribute__((always_inline)) {
-    if (m >= 1 && m - 1 < nt) wait_vmcnt<2 * NLD + 1>();
-    else wait_vmcnt<0>();
+  // later: idle, (M0 V0)..(M_ns-1 V_ns-1) M_ns. Both pass 2 ns + 2 barriers. The steady
+  // state M1 .. M_nt-1 is the pipelined pv_qk in a loop of its own; M0 (QK^T only) and
+  // M_nt (P.V only) are peeled off, so that loop holds one matrix-phase variant (two in
+  // one loop body cost ~70 more VGPRs and spilled).
+  auto open_m = [&](int m) __attribute__((always_inline)) {
+    if (m >= 1 && m - 1 < nt) {
+      // all but the previous VALU phase's loads: K and V (and the ids, through the LDS)
+      if (seg_uniform) wait_vmcnt<2 * NLD>();
+      else wait_vmcnt<2 * NLD + 1>();
+    } else {
+      wait_vmcnt<0>();
+    }
     wait_lgkm0();
     __builtin_amdgcn_s_barrier();
-    mfma_phase_begin();
-    if (m >= 1 && m - 1 < nt) pv(m - 1);  // first: P's registers then hold S
-    // Nothing crosses: the V^T and K fragments of the two products are never all live.
-    __builtin_amdgcn_sched_barrier(0);
-    if (m < nt) qk(m);
-    mfma_phase_end();
   };
   auto interval_v = [&](int m) __attribute__((always_inline)) {
     if (m < nt) wait_vmcnt<2 * NLD>();
     wait_lgkm0();
     __builtin_amdgcn_s_barrier();
     if (m >= nt) return;
+#if PKV_PREFILL_VALU_PRIO == 1
+    __builtin_amdgcn_s_setprio(1);
+#endif
     issue_ids(m + 3);
     issue_tile(m + 1, 1);
     issue_tile(m + 2, 0);
     softmax(tbeg + m, tbeg + m >= j_mask);
+#if PKV_PREFILL_VALU_PRIO == 1
+    __builtin_amdgcn_s_setprio(0);
+#endif
   };
-  if (half == 0) {
-    for (int m = 0; m <= ns; ++m) {
-      interval_m(m);
-      interval_v(m);
-    }
-  } else {
+  const int v_last = half ? ns - 1 : ns;  // this half's last VALU interval
+#if PKV_PREFILL_VALU_PRIO == 2
+  if (half) __builtin_amdgcn_s_setprio(1);
+#endif
+  if (half) {
     wait_lgkm0();
     __builtin_amdgcn_s_barrier();
-    for (int m = 0; m < ns; ++m) {
-      interval_m(m);
-      interval_v(m);
+  }
+  open_m(0);
+  mfma_phase_begin();
+  if (nt > 0) qk(0);
+  mfma_phase_end();
+  if (v_last >= 0) interval_v(0);
+  for (int m = 1; m < nt; ++m) {
+    open_m(m);
+    mfma_phase_begin();
+    pv_qk(m - 1, m);
+    mfma_phase_end();
+    interval_v(m);
+  }
+  for (int m = max(nt, 1); m <= ns; ++m) {
+    open_m(m);
+    if (m == nt) {
+      mfma_phase_begin();
+      pv(m - 1);
+      mfma_phase_end();
     }
-    interval_m(ns);
+    if (m <= v_last) interval_v(m);
   }
 
   // Merge the halves' softmax states through LDS (the rings are free now): half 1
@@ -682,7 +848,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
     for (int t = 0; t < RT; ++t) {
       float* x = xch + t * (2 + 4 * DTL) * kWave;
       x[0] = m_run[t];
-      x[kWave] = l_run[t];
+      x[kWave] = o[t][DTL][0];
 #pragma unroll
       for (int d = 0; d < DTL; ++d)
 #pragma unroll
@@ -700,7 +866,8 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
     const float sa = __builtin_amdgcn_exp2f(m_run[t] - mref);
     const float sb = __builtin_amdgcn_exp2f(mb - mref);
     m_run[t] = mn;
-    l_run[t] = l_run[t] * sa + x[kWave] * sb;
+    const float l_sum = o[t][DTL][0] * sa + x[kWave] * sb;
+    o[t][DTL][0] = l_sum;
 #pragma unroll
     for (int d = 0; d < DTL; ++d)
 #pragma unroll
@@ -710,7 +877,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
   // O^T lane (row col, grp) holds dims 16 d + 4 grp + r of query row col.
 #pragma unroll
   for (int t = 0; t < RT; ++t) {
-    const float l_tot = rows_sum(l_run[t]);
+    const float l_tot = o[t][DTL][0];  // the whole row's sum, in every lane of its column
     if (!row_ok[t]) continue;
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     const int rho = rho0 + 16 * RT * wave + 16 * t + col;
