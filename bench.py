@@ -9,9 +9,10 @@ L independent layer pools (default 4, ~1 GB each at config 2) are used in rotati
 every step reads K/V the previous step did not touch, as consecutive layers of a model
 do; the 256 MB last-level cache cannot serve them.
 
-Timing. ``value`` is the mean time per layer-step when the L layer-steps are captured in
-one hipGraph and replayed (the reference runs decode steps as CUDA-graph replays,
-engine/runtime/cuda_graphs.py), between events bracketed by synchronize(). ``eager_us``
+Timing. ``value`` is the mean time per layer-step over exactly ``--steps`` layer-steps
+(the L pools in rotation) captured in hipGraphs of at least 32 calls and replayed (the
+reference runs decode steps as CUDA-graph replays, engine/runtime/cuda_graphs.py; a model
+step's graph holds every layer), between events bracketed by synchronize(). ``eager_us``
 is the mean of per-call events around eager calls (includes per-call launch costs).
 ``roofline.achieved`` = algorithmic K+V bytes (sum(ctx) * 2 * nkv * hd * 2 B) / the
 graph-replay time per layer-step. ``cpu_baseline`` times the reference's CPU path (torch
@@ -42,6 +43,8 @@ sys.path.insert(0, os.path.join(ROOT, "inference-engine_amd"))
 HBM_PEAK_GBPS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_traffic.json")
+GRAPH_CALLS = 32  # calls captured per timed hipGraph (see graph_us)
+WARM_SECONDS = 0.3  # untimed load before the first timing (see warm_clocks)
 DECODE_SOURCES = ("common.h", "decode_kernels.h", "decode.hip")  # what the stream pass is built from
 METRIC = "paged decode attn us/layer-step + achieved HBM GB/s (% of 8 TB/s), 3B shape"
 
@@ -153,6 +156,17 @@ def traffic_of(step_name: str) -> tuple[int | None, str]:
     return entry["bytes"], f"{entry['source']} (sources {h.hexdigest()[:12]})"
 
 
+def warm_clocks(torch, fns, seconds: float = WARM_SECONDS) -> None:
+    """Untimed calls of the workload itself until `seconds` of wall time passed: the GPU's
+    clock ramps up over tens of milliseconds of load, and a timing taken right after a few
+    milliseconds of warm-up read up to ~10% slow at config 5."""
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for f in fns:
+            f()
+        torch.cuda.synchronize()
+
+
 def eager_us(torch, fns, steps: int, warmup: int) -> list[float]:
     """Per-call event times (µs) of fns called round-robin."""
     for i in range(warmup):
@@ -169,31 +183,49 @@ def eager_us(torch, fns, steps: int, warmup: int) -> list[float]:
 
 
 def graph_us(torch, fns, steps: int, warmup: int) -> tuple[float, float]:
-    """Capture fns (one pass) in a hipGraph and replay it until `steps` calls ran.
-    Returns (µs per call -- per element of fns, wall seconds of the timed region)."""
+    """Time exactly `steps` calls of fns (round-robin) as hipGraph replays: a graph of at
+    least GRAPH_CALLS calls replayed steps // G times, then one graph of the remaining
+    calls. A real engine replays a whole multi-layer step per graph; with a few calls per
+    graph the host's launch of each replay (~40 µs here) outlasts the GPU work and its gap
+    would land in the per-call time. Returns (µs per call, wall seconds of the timed
+    region)."""
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
         for f in fns:
             f()
     torch.cuda.current_stream().wait_stream(side)
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for f in fns:
-            f()
-    for _ in range(max(1, warmup // len(fns))):
+    steps = max(1, steps)
+    g_calls = min(steps, len(fns) * max(1, -(-GRAPH_CALLS // len(fns))))
+    full, rem = divmod(steps, g_calls)
+
+    def capture(n):
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for i in range(n):
+                fns[i % len(fns)]()
+        return graph
+
+    graph = capture(g_calls)
+    tail = capture(rem) if rem else None
+    # at least three untimed replays: the first replays of a process's first graph ran
+    # ~8% slow at config 5 even after warm_clocks (one-time set-up of graph execution)
+    for _ in range(max(3, -(-warmup // g_calls))):
         graph.replay()
-    reps = max(1, steps // len(fns))
+    if tail is not None:
+        tail.replay()
     torch.cuda.synchronize()
     a, z = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     a.record()
-    for _ in range(reps):
+    for _ in range(full):
         graph.replay()
+    if tail is not None:
+        tail.replay()
     z.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    return a.elapsed_time(z) * 1e3 / (reps * len(fns)), wall
+    return a.elapsed_time(z) * 1e3 / steps, wall
 
 
 def decode_setup(args, torch):
@@ -233,6 +265,7 @@ def bench_decode(args, torch) -> dict:
             num_workgroups=wgs)  # fmt: skip
 
     fns = [attn_fn(k, v) for k, v in pools]
+    warm_clocks(torch, fns)
     per = eager_us(torch, fns, args.steps, args.warmup)
     eager_mean = statistics.fmean(per)
     if args.no_graph:
@@ -475,6 +508,7 @@ def bench_mixed(args, torch) -> dict:
                                   d.block_size, out=out_d, num_workgroups=wgs)  # fmt: skip
 
     append()
+    warm_clocks(torch, [append, prefill, decode])
     t_pre = graph_us(torch, [prefill] * 4, args.steps, args.warmup)[0]
     t_dec = graph_us(torch, [decode] * 4, args.steps, args.warmup)[0]
     t_app = graph_us(torch, [append] * 4, args.steps, args.warmup)[0]
