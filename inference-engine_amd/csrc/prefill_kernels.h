@@ -49,6 +49,12 @@ struct PrefillArgs {
 #endif
 // Wave priority (s_setprio): 1 raises the softmax phase's, 2 raises half 1's waves'
 // (younger, so otherwise second in issue arbitration), 0 leaves both at 0.
+// 1: a VALU phase whose two tiles take the 16-token-block fast path fetches both tiles'
+// block ids before waiting on either (one scalar-load round trip, not two; measured
+// 0.7% faster at config 5); 0: one fetch and wait per tile.
+#ifndef PKV_PREFILL_IDS2
+#define PKV_PREFILL_IDS2 1
+#endif
 #ifndef PKV_PREFILL_VALU_PRIO
 #define PKV_PREFILL_VALU_PRIO 0
 #endif
@@ -411,6 +417,19 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
   const uint32_t pool_blocks = (uint32_t)min(a.num_slots / a.bs, (int64_t)0x7FFFFFFF);
   const char* kv_base[2] = {reinterpret_cast<const char*>(a.k) + kvh_bytes,
                             reinterpret_cast<const char*>(a.v) + kvh_bytes};
+  // The 16-token-block fast path of K (kv = 0) or V (kv = 1) of local tile m, with the
+  // tile's four block ids already fetched (v4).
+  auto issue_fast = [&](int m, int kv, const i32x4_a4 v4) __attribute__((always_inline)) {
+    const int j = gtile(m);
+    const uint32_t dst = ring_lds + (uint32_t)(((kv * 2 + (m & 1)) * TILE) * 16);
+    const char* base = kv_base[kv] + (uint32_t)(((j * KT) & (a.bs - 1)) * a.kv_ss * (int)sizeof(S));
+#pragma unroll
+    for (int r = 0; r < NLD; ++r) {
+      uint32_t bid = (uint32_t)__builtin_amdgcn_readfirstlane(v4[r & 3]);
+      bid = bid < pool_blocks ? bid : 0u;  // memory safety only
+      dma16_to_lds_s(base + (uint64_t)bid * blk_bytes32, lane_off[r], dst + (uint32_t)(r * 256 * 16));
+    }
+  };
   // K (kv = 0) or V (kv = 1) of local tile m into stage m % 2.
   auto issue_tile = [&](int m, int kv) __attribute__((always_inline)) {
     const int j = gtile(m);
@@ -796,8 +815,20 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
     __builtin_amdgcn_s_setprio(1);
 #endif
     issue_ids(m + 3);
+#if PKV_PREFILL_IDS2
+    if (POW2 && fast && CH == 16 && NLD == 4 && a.bs_shift == 4 && (gtile(m + 2) + 1) * KT <= n) {
+      const i32x4_a4 v1 = sid4(blk_of(gtile(m + 1) * KT));
+      const i32x4_a4 v2 = sid4(blk_of(gtile(m + 2) * KT));
+      issue_fast(m + 1, 1, v1);
+      issue_fast(m + 2, 0, v2);
+    } else {
+      issue_tile(m + 1, 1);
+      issue_tile(m + 2, 0);
+    }
+#else
     issue_tile(m + 1, 1);
     issue_tile(m + 2, 0);
+#endif
     softmax(tbeg + m, tbeg + m >= j_mask);
 #if PKV_PREFILL_VALU_PRIO == 1
     __builtin_amdgcn_s_setprio(0);
