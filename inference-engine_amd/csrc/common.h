@@ -45,6 +45,11 @@ constexpr int kWave = 64;
 #ifndef PKV_DECODE_COMBINE_SPLIT_PAIRS
 #define PKV_DECODE_COMBINE_SPLIT_PAIRS 2048
 #endif
+// 1: the MFMA stream-K decode pass at head_dim 64 runs P.V on the matrix cores; 0: on
+// the VALU.
+#ifndef PKV_DECODE_PV_MFMA
+#define PKV_DECODE_PV_MFMA 1
+#endif
 // One-launch cascade: the share of the unit stream each prefix workgroup takes after its
 // prefix items, in eighths of a stream workgroup's share (measured at config 3: 2 against
 // 0, 1, 3 and 4).
@@ -207,6 +212,47 @@ template <int W> __device__ __forceinline__ float across_sum_exact(float x) {
 }
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;  // LDS operand of ds_read_tr16_b64
+
+// Eight fp32 probabilities as the P operand fragment of a 16x16x32 MFMA (four dwords of
+// 16-bit pairs) in the K/V type. bf16: hi = bf16(p) (v_cvt_pk_bf16_f32, round to nearest
+// even) plus lo = bf16(p - hi), two MFMAs -- p - hi is exact, and one bf16 rounding of P
+// (8 significant bits) misses a 2e-3 bar on peaked attention. fp16: one rounding (11
+// bits), lo zero -- or, with LO16, lo = fp16(p - hi) as well (22 bits: results then do
+// not depend on where a context is cut into pieces, beyond fp32 rounding).
+template <int DT, bool LO16 = false>
+__device__ __forceinline__ void pack_p8(const float* p, u32x4& hi, u32x4& lo) {
+  if constexpr (DT == PKV_BF16) {
+    typedef __bf16 v2 __attribute__((ext_vector_type(2)));
+    uint32_t h[4], l[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      h[i] = __builtin_bit_cast(uint32_t, v2{(__bf16)p[2 * i], (__bf16)p[2 * i + 1]});
+      // the empty asm keeps h[i] one value (no second conversion to rebuild its low half);
+      // on h[i] itself, so no copy of it is made
+      __asm__("" : "+v"(h[i]));
+      const float r0 = p[2 * i] - __uint_as_float(h[i] << 16);
+      const float r1 = p[2 * i + 1] - __uint_as_float(h[i] & 0xFFFF0000u);
+      l[i] = __builtin_bit_cast(uint32_t, v2{(__bf16)r0, (__bf16)r1});
+    }
+    hi = u32x4{h[0], h[1], h[2], h[3]};
+    lo = u32x4{l[0], l[1], l[2], l[3]};
+  } else {
+    typedef _Float16 v2 __attribute__((ext_vector_type(2)));
+    uint32_t h[4], l[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const v2 hp = v2{(_Float16)p[2 * i], (_Float16)p[2 * i + 1]};
+      h[i] = __builtin_bit_cast(uint32_t, hp);
+      if constexpr (LO16)  // p - hi is exact in fp32
+        l[i] = __builtin_bit_cast(uint32_t, v2{(_Float16)(p[2 * i] - (float)hp[0]),
+                                               (_Float16)(p[2 * i + 1] - (float)hp[1])});
+    }
+    hi = u32x4{h[0], h[1], h[2], h[3]};
+    lo = u32x4{l[0], l[1], l[2], l[3]};
+  }
+}
 
 // Lane h of every 16-lane row, broadcast to its row (DPP row_newbcast).
 template <int H> __device__ __forceinline__ float row_bcast(float x) {

@@ -548,6 +548,7 @@ paged_decode_stream_kernel(const DecodeArgs a) {
 
 template <int DT> struct Mfma16x16x32;
 template <> struct Mfma16x16x32<PKV_BF16> {
+  static constexpr bool kSplit = true;  // P.V on the matrix cores: P as hi + lo (pack_p8)
   typedef __bf16 v8 __attribute__((ext_vector_type(8)));
   __device__ static f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8, a),
@@ -555,6 +556,7 @@ template <> struct Mfma16x16x32<PKV_BF16> {
   }
 };
 template <> struct Mfma16x16x32<PKV_F16> {
+  static constexpr bool kSplit = true;  // P.V on the matrix cores: P as hi + lo (pack_p8 LO16)
   typedef _Float16 v8 __attribute__((ext_vector_type(8)));
   __device__ static f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8, a),
@@ -660,6 +662,20 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs& a, const int 
   static_assert(GPW >= 1 && GPW <= 4, "at most 4 query heads per wave");
   using S = typename Elt<DT>::S;
   using MMA = Mfma16x16x32<DT>;
+  // hd 64: P.V on the matrix cores (PKV_DECODE_PV_MFMA; 5.6% faster than the VALU form,
+  // a row broadcast and 8 FMAs per query head and V row, at config 2's batch and
+  // contexts; at hd 128, a timing copy without any P.V ran only 1% faster, so it keeps
+  // the VALU form). Each wave stages its step's V rows (32 tokens x 64 dims, 4 KiB)
+  // in its own LDS slot, reads them back as V^T operand fragments with transpose reads,
+  // and multiplies them by P^T: the lane's own probabilities, in the order the transpose
+  // delivers the tokens, as a hi + lo pair in either 16-bit type (fp32-like P, as the
+  // VALU form had: every work split then agrees to fp32 rounding). O^T lane (head col,
+  // grp) holds dims 16 d + 4 grp + r.
+  // (The stream-K pass only: the split pass's few short steps per wave are latency-bound,
+  // and the LDS round trip cost config 1 0.2 us.)
+  constexpr bool PVM = HD == 64 && !SPLIT && PKV_DECODE_PV_MFMA;
+  __shared__ __align__(16) u32x4 v_lds[PVM ? PKV_DECODE_WAVES_PER_WG * 256 : 1];
+  char* const vslot = reinterpret_cast<char*>(&v_lds[PVM ? (threadIdx.x / kWave) * 256 : 0]);
 
   const int lane = threadIdx.x & (kWave - 1);
   // Stream-K: wave = task (KV head and head sub-group), workgroup x = unit range.
@@ -928,14 +944,44 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs& a, const int 
       else return load_pair(tb, kr, vr);
     };
 
-    float m_run = -INFINITY;  // running max of head column col (same in all 4 rows)
+    float m_run = -INFINITY;  // exponent reference of head column col (same in all 4 rows)
     float l_run = 0.f;        // this row's share of the running sum
     float acc[GPW][8];
 #pragma unroll
     for (int g = 0; g < GPW; ++g)
 #pragma unroll
       for (int d = 0; d < 8; ++d) acc[g][d] = 0.f;
+    f32x4 ov[PVM ? 4 : 1];  // PVM: O^T, dims 16 d .. 16 d + 15
+#pragma unroll
+    for (int d = 0; d < (PVM ? 4 : 1); ++d) ov[d] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+    // The exponent reference of head column col is raised only when a tile's maximum
+    // exceeds it by more than 2^8 (or it is still -inf): a stale reference changes
+    // nothing in acc / l (both carry the same factor) and keeps p <= 256, and most tiles
+    // then skip the rescale of the accumulators. Returns the reference to subtract (0
+    // while every score so far was masked).
+    auto raise_ref = [&](float mx) __attribute__((always_inline)) {
+      const bool raise = mx > m_run + 8.f;  // m_run = -inf: any live score raises
+      if (__builtin_amdgcn_ballot_w64(raise)) {  // wave-uniform
+        const float mn = raise ? mx : m_run;
+        // mn = -inf only where m_run stays -inf (acc, l are 0 there): factor 1
+        const float alpha = mn == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_run - mn);
+        m_run = mn;
+        l_run *= alpha;
+        if constexpr (PVM) {  // O^T column col is head col: its own factor
+#pragma unroll
+          for (int d = 0; d < 4; ++d) ov[d] *= alpha;
+        } else {
+#pragma unroll
+          for (int g = 0; g < GPW; ++g) {
+            const float al = row_bcast(alpha, g);
+#pragma unroll
+            for (int d = 0; d < 8; ++d) acc[g][d] *= al;
+          }
+        }
+      }
+      return m_run == -INFINITY ? 0.f : m_run;
+    };
     auto tile = [&](const u32x4* kr, const u32x4* vr, unsigned ok) {
       if constexpr (NS == 1) {
         f32x4 s = {0.f, 0.f, 0.f, 0.f};
@@ -948,22 +994,15 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs& a, const int 
           p[r] = ((ok >> r) & 1u) ? s[r] * a.scale_log2 : -INFINITY;
           mx = fmaxf(mx, p[r]);
         }
-        mx = rows_max(mx);
-        const float mn = fmaxf(m_run, mx);
-        const float mref = mn == -INFINITY ? 0.f : mn;  // all masked so far: stay at 0
-        const float alpha = __builtin_amdgcn_exp2f(m_run - mref);
-        m_run = mn;
+        const float mref = raise_ref(rows_max(mx));
   #pragma unroll
         for (int r = 0; r < 4; ++r) p[r] = __builtin_amdgcn_exp2f(p[r] - mref);
-        l_run = __builtin_fmaf(l_run, alpha, (p[0] + p[1]) + (p[2] + p[3]));
+        l_run += (p[0] + p[1]) + (p[2] + p[3]);
         float vf[4][8];
   #pragma unroll
         for (int r = 0; r < 4; ++r) unpack16v<DT>(vr[r], vf[r]);
   #pragma unroll
         for (int g = 0; g < GPW; ++g) {
-          const float al = row_bcast(alpha, g);
-  #pragma unroll
-          for (int d = 0; d < 8; ++d) acc[g][d] *= al;
   #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const float pr = row_bcast(p[r], g);
@@ -972,6 +1011,35 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs& a, const int 
           }
         }
       } else {
+        // PVM: the step's V goes through the wave's LDS slot first, so the transpose
+        // reads' latency runs under the scores and the softmax. V rows: tokens 16 u +
+        // 4 grp + r of the step (u = the lane's sub-tile), 16-byte chunk col % 8 of the
+        // row, at byte 128 tk + 16 (c ^ (tk % 8)) (the transpose reads then hit distinct
+        // banks). V^T fragment d: lane (dim 16 d + col, grp) gets tokens 4 grp .. + 3 of
+        // each sub-tile h2 -- it addresses token 4 grp + col / 4 of sub-tile h2, dims
+        // 16 d + 4 (col % 4) .. + 3 (chunk 2 d + (col % 4) / 2, half (col % 4) % 2).
+        u32x4 vtf[PVM ? 4 : 1];
+        if constexpr (PVM) {
+          const int u = vlane0 ? 0 : 1, c = col & 7;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int tk = 16 * u + 4 * grp + r;
+            *reinterpret_cast<u32x4*>(vslot + tk * 128 + ((c ^ (tk & 7)) << 4)) = vr[r];
+          }
+          const int c4 = col & 3, tr = 4 * grp + (col >> 2);
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2) {
+              const int off = (16 * h2 + tr) * 128 + (((2 * d + (c4 >> 1)) ^ (tr & 7)) << 4) + ((c4 & 1) << 3);
+              const s16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vslot + off));
+              const uint32_t lo = (uint32_t)(uint16_t)x[0] | ((uint32_t)(uint16_t)x[1] << 16);
+              const uint32_t hi = (uint32_t)(uint16_t)x[2] | ((uint32_t)(uint16_t)x[3] << 16);
+              if (h2 == 0) { vtf[d].x = lo; vtf[d].y = hi; } else { vtf[d].z = lo; vtf[d].w = hi; }
+            }
+          }
+          __builtin_amdgcn_sched_barrier(0);  // the reads stay ahead of the scores
+        }
         float p[2][4];
         float mx = -INFINITY;
 #pragma unroll
@@ -985,25 +1053,32 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs& a, const int 
             mx = fmaxf(mx, p[u][r]);
           }
         }
-        mx = rows_max(mx);
-        const float mn = fmaxf(m_run, mx);
-        const float mref = mn == -INFINITY ? 0.f : mn;  // all masked so far: stay at 0
-        const float alpha = __builtin_amdgcn_exp2f(m_run - mref);
-        m_run = mn;
+        const float mref = raise_ref(rows_max(mx));
 #pragma unroll
         for (int u = 0; u < 2; ++u)
 #pragma unroll
           for (int r = 0; r < 4; ++r) p[u][r] = __builtin_amdgcn_exp2f(p[u][r] - mref);
-        l_run = __builtin_fmaf(l_run, alpha, ((p[0][0] + p[0][1]) + (p[0][2] + p[0][3])) +
-                                             ((p[1][0] + p[1][1]) + (p[1][2] + p[1][3])));
+        l_run += ((p[0][0] + p[0][1]) + (p[0][2] + p[0][3])) +
+                 ((p[1][0] + p[1][1]) + (p[1][2] + p[1][3]));
+        if constexpr (PVM) {
+          // P^T: lane (head col, grp) holds tokens 4 grp + r of sub-tile 0, then of
+          // sub-tile 1 -- the order of the two transpose reads of each V^T fragment.
+          float p8[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) p8[e] = p[e / 4][e % 4];
+          u32x4 phi, plo;
+          pack_p8<DT, true>(p8, phi, plo);
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            ov[d] = MMA::mma(vtf[d], phi, ov[d]);
+            if constexpr (MMA::kSplit) ov[d] = MMA::mma(vtf[d], plo, ov[d]);
+          }
+        } else {
         float vf[4][8];
 #pragma unroll
         for (int r = 0; r < 4; ++r) unpack16v<DT>(vr[r], vf[r]);
 #pragma unroll
         for (int g = 0; g < GPW; ++g) {
-          const float al = row_bcast(alpha, g);
-#pragma unroll
-          for (int d = 0; d < 8; ++d) acc[g][d] *= al;
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             // This lane's V rows are sub-tile (col / 8)'s: that sub-tile's weights. Both
@@ -1014,6 +1089,7 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs& a, const int 
 #pragma unroll
             for (int d = 0; d < 8; ++d) acc[g][d] = __builtin_fmaf(pr, vf[r][d], acc[g][d]);
           }
+        }
         }
       }
     };
@@ -1053,13 +1129,28 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs& a, const int 
     // Totals: l over the four rows of each column, acc over the four rows (and, at hd 64,
     // over the two sub-tiles' lane columns c and c + 8, which hold the same dims).
     const float l_tot = rows_sum(l_run);
+    if constexpr (PVM) {
+      // O^T (already summed over every token) to acc's layout below -- lanes grp 0, col
+      // < 8: head g's dims 8 col .. 8 col + 7 -- through the wave's slot, after the last
+      // step's reads of it (LDS keeps one wave's accesses in order).
+      float* xs = reinterpret_cast<float*>(vslot);  // [GPW][64]
+      if (col < GPW) {
 #pragma unroll
-    for (int g = 0; g < GPW; ++g)
-#pragma unroll
-      for (int d = 0; d < 8; ++d) {
-        acc[g][d] = rows_sum(acc[g][d]);
-        if constexpr (NS == 2) acc[g][d] += dpp<kRowRor8>(acc[g][d]);  // lanes c, c ^ 8
+        for (int d = 0; d < 4; ++d) *reinterpret_cast<f32x4*>(xs + col * 64 + 16 * d + 4 * grp) = ov[d];
       }
+#pragma unroll
+      for (int g = 0; g < GPW; ++g)
+#pragma unroll
+        for (int d = 0; d < 8; ++d) acc[g][d] = (grp == 0 && col < 8) ? xs[g * 64 + 8 * col + d] : 0.f;
+    } else {
+#pragma unroll
+      for (int g = 0; g < GPW; ++g)
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {
+          acc[g][d] = rows_sum(acc[g][d]);
+          if constexpr (NS == 2) acc[g][d] += dpp<kRowRor8>(acc[g][d]);  // lanes c, c ^ 8
+        }
+    }
     float lh[GPW], mh[GPW];
 #pragma unroll
     for (int g = 0; g < GPW; ++g) {

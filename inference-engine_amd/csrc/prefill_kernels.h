@@ -94,8 +94,6 @@ using namespace pkv;
 // accuracy), for fp16 rounded once.
 // ---------------------------------------------------------------------------------
 
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 template <int DT> struct Mfma16x16x32Bits;  // MFMA on raw 16-bit bit patterns
 template <> struct Mfma16x16x32Bits<PKV_BF16> {
@@ -109,16 +107,16 @@ template <> struct Mfma16x16x32Bits<PKV_BF16> {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8, a),
                                                    __builtin_bit_cast(v8, b), c, 0, 0, 0);
   }
-  // 8 finite fp32 -> hi and lo operand fragments (v_cvt_pk_bf16_f32, round to nearest
-  // even); lo = p - hi is exact.
+  // 8 finite fp32 -> hi and lo operand fragments (pack_p8: v_cvt_pk_bf16_f32, round to
+  // nearest even; lo = p - hi is exact).
   __device__ static void pack8(const float* p, u32x4& hi, u32x4& lo) {
-    uint32_t h[4], l[4];
 #if PKV_PREFILL_DOT2LO
     // lo from one v_dot2c_f32_bf16 per value (p + hi_pair . (-1, 0)). The pairs (-1, 0)
     // and (0, -1) go in as registers with these exact bits: left to itself the compiler
     // encodes the first as the inline constant -1.0, whose 32-bit pattern is the second
-    // pair (lo of p0 then came out as p0 - hi of p1). Measured slower than the two plain
-    // instructions per value below (the dot product issues at a lower rate).
+    // pair (lo of p0 then came out as p0 - hi of p1). Measured slower than pack_p8's two
+    // plain instructions per value (the dot product issues at a lower rate).
+    uint32_t h[4], l[4];
     uint32_t neg_lo = 0x0000BF80u, neg_hi = 0xBF800000u;
     __asm__("" : "+v"(neg_lo), "+v"(neg_hi));
     const v2 c0 = __builtin_bit_cast(v2, neg_lo), c1 = __builtin_bit_cast(v2, neg_hi);
@@ -130,20 +128,11 @@ template <> struct Mfma16x16x32Bits<PKV_BF16> {
       const float r1 = __builtin_amdgcn_fdot2_f32_bf16(hp, c1, p[2 * i + 1], false);
       l[i] = __builtin_bit_cast(uint32_t, v2{(__bf16)r0, (__bf16)r1});
     }
-#else
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      h[i] = __builtin_bit_cast(uint32_t, v2{(__bf16)p[2 * i], (__bf16)p[2 * i + 1]});
-      // the empty asm keeps h[i] one value (no second conversion to rebuild its low half);
-      // on h[i] itself, so no copy of it is made
-      __asm__("" : "+v"(h[i]));
-      const float r0 = p[2 * i] - __uint_as_float(h[i] << 16);
-      const float r1 = p[2 * i + 1] - __uint_as_float(h[i] & 0xFFFF0000u);
-      l[i] = __builtin_bit_cast(uint32_t, v2{(__bf16)r0, (__bf16)r1});
-    }
-#endif
     hi = u32x4{h[0], h[1], h[2], h[3]};
     lo = u32x4{l[0], l[1], l[2], l[3]};
+#else
+    pack_p8<PKV_BF16>(p, hi, lo);
+#endif
   }
 };
 template <> struct Mfma16x16x32Bits<PKV_F16> {
