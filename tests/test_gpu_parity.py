@@ -235,6 +235,32 @@ def test_decode_head_dims_and_groups(hd, groups):
     _check_attention(step, what=f"hd{hd} g{groups}")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("groups", [1, 2, 3, 4, 5, 8])
+@pytest.mark.parametrize("block_size", [16, 12])
+def test_decode_hd64_stream_pass_matrix_pv(dtype, groups, block_size):
+    """The stream-K pass at head_dim 64 multiplies P.V on the matrix cores (each wave's V
+    rows staged in LDS and read back transposed, P as a hi + lo pair): oracle parity over
+    1-4 query heads per wave and sub-groups, tile-aligned and tile-splitting block sizes,
+    ragged, tile-boundary and empty contexts, several work splits (pieces cut anywhere),
+    and agreement with the one-launch split pass (P.V on the VALU) to fp32 rounding."""
+    _say("decode hd64 stream pass", dtype, groups, block_size)
+    nkv = 2
+    ctx = [0, 1, 15, 16, 17, 31, 32, 33, 250, 1000, 1999]
+    step = workloads.custom(ctx, nkv * groups, nkv, 64, block_size, dtype, DEV,
+                            seed=64 + groups + block_size)  # fmt: skip
+    for wgs in (2, 7, 64):
+        out32, _ = _check_attention(step, wgs=wgs, what=f"g{groups} bs{block_size} wgs{wgs}")
+        assert not out32[0].any()  # empty context: 0
+    if pa.default_workgroups(DEV, dtype, 64, nkv * groups, nkv, len(ctx),
+                             step.block_tables.shape[1], block_size) == 0:  # fmt: skip
+        split = torch.empty_like(out32)
+        pa.paged_decode_attention(step.q, step.k_cache, step.v_cache, step.block_tables,
+                                  step.context_lens, block_size, out=split)  # fmt: skip
+        torch.cuda.synchronize()
+        assert (out32 - split).abs().max().item() <= 1e-5
+
+
 @pytest.mark.parametrize("block_size", [1, 2, 3, 8, 32])
 def test_decode_block_sizes(block_size):
     _say("decode block size", block_size)
