@@ -1069,9 +1069,13 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs& a, const int 
         if constexpr (PVM) {
           // P^T: lane (head col, grp) holds tokens 4 grp + r of sub-tile 0, then of
           // sub-tile 1 -- the order of the two transpose reads of each V^T fragment.
+          // fp16: P scaled by 2^7 (exact; P <= 2^8 keeps it below fp16's maximum), so
+          // that weights down to ~5e-10 stay above fp16's smallest subnormal instead of
+          // flushing to zero; the epilogue scales O back.
+          constexpr float kPScale = DT == PKV_F16 ? 128.f : 1.f;
           float p8[8];
 #pragma unroll
-          for (int e = 0; e < 8; ++e) p8[e] = p[e / 4][e % 4];
+          for (int e = 0; e < 8; ++e) p8[e] = p[e / 4][e % 4] * kPScale;
           u32x4 phi, plo;
           pack_p8<DT, true>(p8, phi, plo);
 #pragma unroll
@@ -1140,9 +1144,11 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeArgs& a, const int 
       // < 8: head g's dims 8 col .. 8 col + 7 -- through the wave's slot, after the last
       // step's reads of it (LDS keeps one wave's accesses in order).
       float* xs = reinterpret_cast<float*>(vslot);  // [GPW][64]
+      constexpr float kOScale = DT == PKV_F16 ? 1.f / 128.f : 1.f;  // P's fp16 scale undone
       if (col < GPW) {
 #pragma unroll
-        for (int d = 0; d < 4; ++d) *reinterpret_cast<f32x4*>(xs + col * 64 + 16 * d + 4 * grp) = ov[d];
+        for (int d = 0; d < 4; ++d)
+          *reinterpret_cast<f32x4*>(xs + col * 64 + 16 * d + 4 * grp) = ov[d] * kOScale;
       }
 #pragma unroll
       for (int g = 0; g < GPW; ++g)

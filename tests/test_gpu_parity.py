@@ -8,6 +8,7 @@ Each test prints the case it is about to run (flushed) so a failing GPU step nam
 
 from __future__ import annotations
 
+import math
 import os
 
 import pytest
@@ -259,6 +260,31 @@ def test_decode_hd64_stream_pass_matrix_pv(dtype, groups, block_size):
                                   step.context_lens, block_size, out=split)  # fmt: skip
         torch.cuda.synchronize()
         assert (out32 - split).abs().max().item() <= 1e-5
+
+
+def test_decode_hd64_fp16_tiny_weights_keep_their_mass():
+    """fp16 P on the matrix cores: one dominant key and 30,000 keys whose weights (2^-26
+    of it, ~1.5e-8) lie below half of fp16's smallest subnormal. Their V of 8 carries
+    ~3.6e-3 of the output, so weights rounded to zero in fp16 would miss the 2e-3 bar;
+    the kernel scales P by 2^7 before packing it (and O back) so they stay."""
+    _say("decode hd64 fp16 tiny weights")
+    n = 30_001
+    step = workloads.custom([n], 4, 1, 64, 16, torch.float16, DEV, seed=5)
+    step.q.zero_()
+    step.q[:, :, 0] = 16.0
+    step.k_cache.zero_()
+    step.v_cache.fill_(8.0)
+    dom = int(step.block_tables[0, 0]) * 16  # token 0's slot
+    # score difference 16 * 9 = 144, times scale * log2(e) = 0.125 * 1.4427: ~26 in log2
+    step.k_cache[dom, :, 0] = 9.0
+    step.v_cache[dom] = 0.0
+    # one workgroup: every key in the dominant key's piece (other pieces would take
+    # their own exponent reference, where these weights are not small)
+    out32, err = _check_attention(step, wgs=1, what="tiny weights")
+    w = 2.0 ** (-144 * 0.125 / math.log(2))
+    want = 8 * (n - 1) * w / (1 + (n - 1) * w)
+    assert want > 3e-3
+    assert abs(out32[0, 0, 0].item() - want) < 2e-4
 
 
 @pytest.mark.parametrize("block_size", [1, 2, 3, 8, 32])
