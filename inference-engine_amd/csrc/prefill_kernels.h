@@ -103,6 +103,7 @@ template <> struct Mfma16x16x32Bits<PKV_BF16> {
   // P enters the product as hi = bf16(P) plus lo = bf16(P - hi) (two MFMAs).
   static constexpr bool kSplit = true;
   static constexpr uint32_t kOnePair = 0x3F803F80u;  // two bf16 1.0
+  static constexpr float kPLog2 = 0.f;  // bf16's exponent range holds every weight
   __device__ static f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8, a),
                                                    __builtin_bit_cast(v8, b), c, 0, 0, 0);
@@ -140,6 +141,11 @@ template <> struct Mfma16x16x32Bits<PKV_F16> {
   typedef _Float16 v2 __attribute__((ext_vector_type(2)));
   static constexpr bool kSplit = false;  // fp16 keeps 11 bits: P rounded once
   static constexpr uint32_t kOnePair = 0x3C003C00u;  // two fp16 1.0
+  // P carries a factor 2^kPLog2 (folded into the exponent's offset): weights down to
+  // 2^-31 of the reference stay at or above fp16's smallest subnormal (2^-24) instead of
+  // rounding to zero, and the largest, below 2^(8 + 7), stays below fp16's maximum. The
+  // row sums carry the same factor, so O / l is unchanged; the log-sum-exp takes it out.
+  static constexpr float kPLog2 = 7.f;
   __device__ static f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8, a),
                                                   __builtin_bit_cast(v8, b), c, 0, 0, 0);
@@ -484,7 +490,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
   };
 
   float m_run[RT];
-  float nref[RT];  // minus the exponent reference: -m_run, or 0 while m_run is -inf
+  float nref[RT];  // the exponent's offset: kPLog2 - m_run, or 0 while m_run is -inf
   // O^T tiles d < DTL; tile DTL is the softmax normaliser: the matrix cores multiply each
   // P^T fragment by an all-ones V^T fragment too, so every lane of row n's column holds
   // row n's sum of the same (hi + lo) weights O carries -- no VALU adds, no cross-lane sum.
@@ -695,9 +701,10 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
   // second copy would double).
   auto softmax = [&](int j, bool masked) __attribute__((always_inline)) {
     const int kt0 = j * KT;
-    // p = exp2(scale_log2 * s - m_run). The reference m_run is raised only when a score
-    // exceeds it by more than 2^8: a stale reference changes nothing in O / l (both carry
-    // the same factor), keeps p <= 256, and leaves O untouched on most tiles. The row
+    // p = exp2(scale_log2 * s - m_run + kPLog2). The reference m_run is raised only when a
+    // score exceeds it by more than 2^8: a stale reference changes nothing in O / l (both
+    // carry the same factor), keeps p <= 2^(8 + kPLog2), and leaves O untouched on most
+    // tiles. The row
     // tiles are independent chains: maxima first, one rescale branch, then every exp.
     float mx[RT];
     bool raise[RT];
@@ -728,7 +735,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
         // half's tiles can all lie past a row's causal limit).
         const float alpha = raise[t] ? __builtin_amdgcn_exp2f(m_run[t] - mx[t]) : 1.f;
         m_run[t] = raise[t] ? mx[t] : m_run[t];
-        nref[t] = raise[t] ? -mx[t] : nref[t];  // a raise sets a finite maximum
+        nref[t] = raise[t] ? MMA::kPLog2 - mx[t] : nref[t];  // a raise sets a finite maximum
 #pragma unroll
         for (int d = 0; d <= DTL; ++d) o[t][d] *= alpha;
       }
@@ -903,7 +910,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
     const int rho = rho0 + 16 * RT * wave + 16 * t + col;
     if (a.lse && grp == 0)  // log2 normaliser: the exponent reference m_run plus log2(sum)
       a.lse[(int64_t)(q0 + rho / G) * a.nh + kvh * G + rho % G] =
-          l_tot > 0.f ? m_run[t] + __log2f(l_tot) : -INFINITY;
+          l_tot > 0.f ? m_run[t] + (__log2f(l_tot) - MMA::kPLog2) : -INFINITY;
     const int64_t e0 = (int64_t)(q0 + rho / G) * a.out_st + (int64_t)(kvh * G + rho % G) * a.out_sh;
 #pragma unroll
     for (int d = 0; d < DTL; ++d) {

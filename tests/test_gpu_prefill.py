@@ -98,15 +98,30 @@ def test_prefill_valu_kernel_shapes(dtype, nh, nkv, hd, bs):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
 def test_prefill_valu_non_causal_rows_and_lse(dtype):
     """pkv_paged_prefill_ex on the VALU kernel: causal = 0 (every query sees the chunk's
-    whole context), queries gathered through q_rows, log2 normalisers. Non-causal
-    attention of one query over n keys is the decode oracle with context n; the
-    normaliser is checked in float64 from its definition."""
+    whole context), queries gathered through q_rows, log2 normalisers."""
+    _say("prefill valu ex", dtype)
+    _check_ex(dtype, 4, 2, 16, 4, [(3, 21), (5, 9)], seed=11)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize(("nh", "nkv", "hd", "bs"), [(8, 2, 128, 16), (4, 1, 64, 12)])
+def test_prefill_matrix_non_causal_rows_and_lse(dtype, nh, nkv, hd, bs):
+    """The same on the matrix-core kernel (the cascade's prefix pass), whose fp16 weights
+    carry a power-of-two factor that its log2 normalisers must leave out; contexts of
+    several key tiles in both key halves."""
+    _say("prefill matrix ex", dtype, nh, nkv, hd, bs)
+    # fp16 weights are rounded once (relative error <= 2^-11 each), so the sum is within
+    # a factor 1 + 2^-11 of the exact one: log2(1 + 2^-11) = 7.04e-4
+    lse_tol = 8e-4 if dtype == torch.float16 else 1e-4
+    _check_ex(dtype, nh, nkv, hd, bs, [(3, 700), (5, 9), (2, 130)], seed=12, lse_tol=lse_tol)
+
+
+def _check_ex(dtype, nh, nkv, hd, bs, spec, seed, lse_tol=1e-4):
+    """Non-causal attention of one query over n keys is the decode oracle with context n;
+    the normaliser is checked in float64 from its definition."""
     from engine.kernels import _native
 
-    _say("prefill valu ex", dtype)
-    nh, nkv, hd, bs = 4, 2, 16, 4
-    spec = [(3, 21), (5, 9)]
-    q, k, v, tables, ctx, cu = _chunks(spec, nh, nkv, hd, bs, dtype, seed=11)
+    q, k, v, tables, ctx, cu = _chunks(spec, nh, nkv, hd, bs, dtype, seed=seed)
     t = q.shape[0]
     rows = torch.randperm(t, generator=torch.Generator().manual_seed(1)).int()
     qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
@@ -117,7 +132,8 @@ def test_prefill_valu_non_causal_rows_and_lse(dtype):
         out.data_ptr(), _native.PKV_F32, out.stride(0), out.stride(1), qd.data_ptr(),
         qd.stride(0), qd.stride(1), kd.data_ptr(), vd.data_ptr(), _native.dtype_code(dtype, "t"),
         kd.stride(0), kd.stride(1), kd.shape[0], td.data_ptr(), td.stride(0), td.shape[1],
-        cd.data_ptr(), cud.data_ptr(), len(spec), 5, nh, nkv, hd, bs, hd**-0.5, 0,
+        cd.data_ptr(), cud.data_ptr(), len(spec), max(a for a, _ in spec), nh, nkv, hd, bs,
+        hd**-0.5, 0,
         rd.data_ptr(), lse.data_ptr(), torch.cuda.current_stream().cuda_stream)  # fmt: skip
     _native.check(st, "prefill_ex")
     torch.cuda.synchronize()
@@ -138,7 +154,7 @@ def test_prefill_valu_non_causal_rows_and_lse(dtype):
             torch.tensor(2.0, dtype=torch.float64))  # log2 units
         ref = torch.logsumexp(sc * torch.log(torch.tensor(2.0, dtype=torch.float64)), 0) / \
             torch.log(torch.tensor(2.0, dtype=torch.float64))  # fmt: skip
-        assert (lse[i].cpu().double() - ref).abs().max().item() <= 1e-4
+        assert (lse[i].cpu().double() - ref).abs().max().item() <= lse_tol, i
 
 
 @pytest.mark.parametrize(("nh", "nkv"), [(32, 8), (24, 8), (8, 8), (16, 1)])
@@ -249,11 +265,10 @@ def test_prefill_many_chunks(n_chunks):
 
 @pytest.mark.parametrize("hd", [64, 128])
 def test_prefill_bf16_values_beyond_fp16(hd):
-    """For bf16 caches the P.V product takes V as fp16 (converted in LDS as each tile
-    lands); a workgroup whose item meets a V value outside fp16's range recomputes the
-    item with the exact bf16 pair. Some V rows of chunks 0 and 2 are scaled by 3e6 and
-    -7e4 (fp16 would hold them as +-inf): every output is finite and within 2e-3 of the
-    oracle relative to the largest |V| its chunk reads, the other chunks within 2e-3."""
+    """bf16 caches keep V in bf16 on the matrix cores: values outside fp16's range pass
+    through. Some V rows of chunks 0 and 2 are scaled by 3e6 and -7e4 (fp16 would hold
+    them as +-inf): every output is finite and within 2e-3 of the oracle relative to the
+    largest |V| its chunk reads, the other chunks within 2e-3."""
     _say("prefill bf16 V beyond fp16", hd)
     spec = [(40, 300), (33, 33), (64, 500), (1, 90)]
     q, k, v, tables, ctx, cu = _chunks(spec, 8, 2, hd, 16, torch.bfloat16, seed=hd)
@@ -271,3 +286,30 @@ def test_prefill_bf16_values_beyond_fp16(hd):
         lo, hi = int(cu[c]), int(cu[c + 1])
         err = (got[lo:hi] - want[lo:hi]).abs().max().item()
         assert err <= ATOL * scale[c], (c, err, scale[c])
+
+
+def test_prefill_fp16_tiny_weights_keep_their_mass():
+    """fp16 P on the matrix cores: one dominant key (the first) and 60,000 keys whose
+    weights (2^-26 of it, ~1.5e-8) lie below half of fp16's smallest subnormal. The first
+    key half's 30,000 of them carry ~3.6e-3 of the output through their V of 8, so
+    weights rounded to zero in fp16 would miss the 2e-3 bar; the kernel's exponent offset
+    scales P by 2^7 so they stay. The second half takes its own exponent reference."""
+    import math
+
+    _say("prefill fp16 tiny weights")
+    n = 60_001
+    q, k, v, tables, ctx, cu = _chunks([(1, n)], 4, 1, 64, 16, torch.float16, seed=6)
+    q.zero_()
+    q[:, :, 0] = 16.0
+    k.zero_()
+    v.fill_(8.0)
+    dom = int(tables[0, 0]) * 16  # key 0's slot
+    # score difference 16 * 9 = 144, times scale * log2(e) = 0.125 * 1.4427: ~26 in log2
+    k[dom, :, 0] = 9.0
+    v[dom] = 0.0
+    got = _run(q, k, v, tables, ctx, cu, 16, 1)
+    w = 2.0 ** (-144 * 0.125 / math.log(2))
+    want = 8 * (n - 1) * w / (1 + (n - 1) * w)
+    assert want > 7e-3
+    err = (got[0] - want).abs().max().item()
+    assert err < 2e-4, err
