@@ -545,7 +545,7 @@ def bench_mixed(args, torch) -> dict:
             "traffic": traffic,
         },
         "traffic_source": traffic_source,
-        "roofline_scope": "pkv_paged_prefill call (matrix-core prefill)",
+        "roofline_scope": "paged_prefill_attention call (fp16 V copy + matrix-core prefill)",
         "prefill_us": round(t_pre, 2),
         "prefill_gflop": round(flops / 1e9, 2),
         "decode_us": round(t_dec, 2),

@@ -300,6 +300,41 @@ int pkv_paged_prefill_ex(void* out, int out_dtype, int64_t out_stride_tok, int64
                          int32_t causal, const int32_t* q_rows, float* lse, void* stream);
 
 /*
+ * Bytes of workspace pkv_paged_prefill_ws needs for the fp16 V copy at these static
+ * shapes: about n_chunks x (max_blocks * block_size rounded up to 256) x num_kv_heads x
+ * head_dim x 2, plus one scale byte per 256 tokens of each. 0 for shapes that take no
+ * copy (fp16 or fp32 caches, head_dim 16, tables of more than 65,536 tokens); negative:
+ * PKV_E_SHAPE. No counterpart in the reference (whose varlen path
+ * gathers each chunk's K and V into new tensors itself).
+ */
+int64_t pkv_prefill_workspace_bytes(int kv_dtype, int32_t head_dim, int32_t num_kv_heads,
+                                    int32_t n_chunks, int32_t max_blocks, int32_t block_size);
+
+/*
+ * pkv_paged_prefill with a workspace; replaces the same reference call (engine/model/
+ * layers.py:246-253). When workspace_bytes >= pkv_prefill_workspace_bytes (> 0) for
+ * these shapes, a first kernel writes each chunk's V (its clamped context, per KV head)
+ * as fp16 into the workspace, each 256-token tile times a power of two 2^-k that keeps
+ * its largest |V| below 2^16 (k = 0 unless some |V| >= 2^16), and the matrix cores then
+ * multiply P by that copy in fp16 (P rounded once, as for fp16 caches) instead of as a
+ * bf16 hi + lo pair: one P.V product instead of two. The scaled bf16 -> fp16 conversion
+ * is exact down to 2^-14 (times 2^k); smaller values keep an absolute error below
+ * 2^-25 (times 2^k). With a smaller workspace (NULL and 0 included) the call is
+ * pkv_paged_prefill. The workspace is scratch (its contents on entry do not matter; the
+ * call overwrites them) and 16-byte aligned (PKV_E_ALIGN otherwise; PKV_E_WORKSPACE for
+ * negative bytes, or bytes without a pointer).
+ */
+int pkv_paged_prefill_ws(void* out, int out_dtype, int64_t out_stride_tok, int64_t out_stride_h,
+                         const void* q, int64_t q_stride_tok, int64_t q_stride_h,
+                         const void* k_cache, const void* v_cache, int kv_dtype,
+                         int64_t kv_stride_slot, int64_t kv_stride_head, int64_t num_slots,
+                         const int32_t* block_tables, int64_t table_stride, int32_t max_blocks,
+                         const int32_t* context_lens, const int32_t* cu_seqlens_q,
+                         int32_t n_chunks, int32_t max_query_len, int32_t num_heads,
+                         int32_t num_kv_heads, int32_t head_dim, int32_t block_size, float scale,
+                         void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * Fused element-wise kernels (csrc/fused.hip). Replace the reference's Triton kernels of
  * engine/kernels/fused.py:47-131 (rms_norm, rope_, silu_mul), with the same contract:
  * every result is bitwise identical to the PyTorch ops they stand for.

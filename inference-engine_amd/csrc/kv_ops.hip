@@ -194,7 +194,7 @@ hipError_t append_out(int dout, bool vec, void* kp, void* vp, int64_t ps_slot,
 
 extern "C" {
 
-int pkv_abi_version(void) { return 4; }
+int pkv_abi_version(void) { return 5; }
 
 const char* pkv_status_string(int status) {
   switch (status) {

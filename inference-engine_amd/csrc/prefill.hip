@@ -212,10 +212,19 @@ hipError_t launch_prefill_hd(PrefillArgs a, int64_t rows, hipStream_t st) {
   const int64_t items = (int64_t)a.row_blocks * a.nkv * a.n_chunks;
   if (items > 0x7FFFFFFF) return hipErrorInvalidValue;
   const dim3 grid((unsigned)items), block(512);
+  if constexpr (DT == PKV_BF16) {
+    if (a.v16) {  // P.V in fp16 against the copy of V
+      if (a.bs_shift >= 0)
+        hipLaunchKernelGGL((paged_prefill_kernel<DT, HD, true, true>), grid, block, 0, st, a);
+      else
+        hipLaunchKernelGGL((paged_prefill_kernel<DT, HD, false, true>), grid, block, 0, st, a);
+      return hipGetLastError();
+    }
+  }
   if (a.bs_shift >= 0)
-    hipLaunchKernelGGL((paged_prefill_kernel<DT, HD, true>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((paged_prefill_kernel<DT, HD, true, false>), grid, block, 0, st, a);
   else
-    hipLaunchKernelGGL((paged_prefill_kernel<DT, HD, false>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((paged_prefill_kernel<DT, HD, false, false>), grid, block, 0, st, a);
   return hipGetLastError();
 }
 
@@ -227,6 +236,21 @@ hipError_t launch_prefill(const PrefillArgs& a, int hd, int64_t rows, hipStream_
     case 128: return launch_prefill_hd<DT, 128>(a, rows, st);
     default: return launch_prefill_hd<DT, 256>(a, rows, st);
   }
+}
+
+// The fp16 V copy ahead of a bf16 matrix-core prefill: grid (region tiles of the widest
+// possible context, KV heads, chunks); workgroups past their chunk's context leave.
+hipError_t launch_v16(const PrefillArgs& a, int hd, hipStream_t st) {
+  const int64_t tiles = ((int64_t)a.max_blocks * a.bs + kV16Rows - 1) / kV16Rows;
+  if (tiles < 1) return hipSuccess;
+  const dim3 grid((unsigned)tiles, (unsigned)a.nkv, (unsigned)a.n_chunks), block(256);
+  switch (hd) {
+    case 32: hipLaunchKernelGGL((prefill_v16_kernel<32>), grid, block, 0, st, a); break;
+    case 64: hipLaunchKernelGGL((prefill_v16_kernel<64>), grid, block, 0, st, a); break;
+    case 128: hipLaunchKernelGGL((prefill_v16_kernel<128>), grid, block, 0, st, a); break;
+    default: hipLaunchKernelGGL((prefill_v16_kernel<256>), grid, block, 0, st, a); break;
+  }
+  return hipGetLastError();
 }
 
 // The VALU kernel: grid (chunks x query tiles, KV heads x head sub-groups).
@@ -323,10 +347,57 @@ int prefill_args(PrefillArgs* out_args, int64_t* rows_out, void* out, int out_dt
   a.lse = lse;
   a.scale_log2 = scale * 1.4426950408889634f;
   a.out_f32 = out_dtype == PKV_F32;
+  a.v16 = nullptr;
+  a.v16_k = nullptr;
+  a.v16_kstride = 0;
   return 0;
 }
 
 }  // namespace pkv
+
+namespace {
+
+// Launches for checked arguments: the matrix cores take 16-bit K/V at head_dim 32..256
+// (a bf16 call with a.v16 set converts the chunks' V first), the VALU kernel the rest.
+int run_prefill(const PrefillArgs& a, int64_t rows, int kv_dtype, int head_dim,
+                int max_query_len, hipStream_t st) {
+  if (kv_dtype == PKV_F32) return (int)launch_rows<PKV_F32>(a, head_dim, max_query_len, st);
+  if (head_dim == 16) {
+    return (int)(kv_dtype == PKV_BF16 ? launch_rows<PKV_BF16>(a, head_dim, max_query_len, st)
+                                      : launch_rows<PKV_F16>(a, head_dim, max_query_len, st));
+  }
+  if (kv_dtype == PKV_F16) return (int)launch_prefill<PKV_F16>(a, head_dim, rows, st);
+  if (a.v16) {
+    const hipError_t e = launch_v16(a, head_dim, st);
+    if (e != hipSuccess) return (int)e;
+  }
+  return (int)launch_prefill<PKV_BF16>(a, head_dim, rows, st);
+}
+
+// Whether a call of these shapes can use the fp16 V copy: bf16 at head_dim 32..256,
+// tables of at most kV16MaxTokens tokens, slot indices within 31 bits.
+bool v16_shapes(int kv_dtype, int head_dim, int32_t max_blocks, int32_t block_size,
+                int64_t num_slots) {
+  return kv_dtype == PKV_BF16 && head_dim >= 32 && head_dim <= 256 &&
+         (int64_t)max_blocks * block_size <= kV16MaxTokens && num_slots <= 0x7FFFFFFF;
+}
+
+// Workspace of the fp16 V copy: the scale exponents (a row of kstride bytes per chunk and
+// KV head, the area rounded up to 256 bytes), then every chunk's region at its widest.
+struct V16Layout {
+  int64_t kstride, k_bytes, total;
+};
+V16Layout v16_layout(int32_t head_dim, int32_t num_kv_heads, int32_t n_chunks,
+                     int32_t max_blocks, int32_t block_size) {
+  const int64_t pad = v16_pad(max_blocks * block_size);
+  V16Layout l;
+  l.kstride = (pad / kV16Rows + 3) / 4 * 4;
+  l.k_bytes = ((int64_t)n_chunks * num_kv_heads * l.kstride + 255) / 256 * 256;
+  l.total = l.k_bytes + (int64_t)n_chunks * pad * num_kv_heads * head_dim * 2;
+  return l;
+}
+
+}  // namespace
 
 extern "C" {
 
@@ -364,15 +435,47 @@ int pkv_paged_prefill_ex(void* out, int out_dtype, int64_t out_stride_tok, int64
                                max_query_len, num_heads, num_kv_heads, head_dim, block_size,
                                scale, causal, q_rows, lse);
   if (bad) return bad == 1 ? 0 : bad;
-  hipStream_t st = (hipStream_t)stream;
-  // The matrix cores take 16-bit K/V at head_dim 32..256; the VALU kernel the rest.
-  if (kv_dtype == PKV_F32) return (int)launch_rows<PKV_F32>(a, head_dim, max_query_len, st);
-  if (head_dim == 16) {
-    return (int)(kv_dtype == PKV_BF16 ? launch_rows<PKV_BF16>(a, head_dim, max_query_len, st)
-                                      : launch_rows<PKV_F16>(a, head_dim, max_query_len, st));
+  return run_prefill(a, rows, kv_dtype, head_dim, max_query_len, (hipStream_t)stream);
+}
+
+int64_t pkv_prefill_workspace_bytes(int kv_dtype, int32_t head_dim, int32_t num_kv_heads,
+                                    int32_t n_chunks, int32_t max_blocks, int32_t block_size) {
+  if (num_kv_heads <= 0 || n_chunks < 0 || max_blocks < 0 || block_size <= 0 ||
+      (int64_t)max_blocks * block_size > (int64_t)1 << 30)
+    return PKV_E_SHAPE;
+  if (!v16_shapes(kv_dtype, head_dim, max_blocks, block_size, 0)) return 0;
+  return v16_layout(head_dim, num_kv_heads, n_chunks, max_blocks, block_size).total;
+}
+
+int pkv_paged_prefill_ws(void* out, int out_dtype, int64_t out_stride_tok, int64_t out_stride_h,
+                         const void* q, int64_t q_stride_tok, int64_t q_stride_h,
+                         const void* k_cache, const void* v_cache, int kv_dtype,
+                         int64_t kv_stride_slot, int64_t kv_stride_head, int64_t num_slots,
+                         const int32_t* block_tables, int64_t table_stride, int32_t max_blocks,
+                         const int32_t* context_lens, const int32_t* cu_seqlens_q,
+                         int32_t n_chunks, int32_t max_query_len, int32_t num_heads,
+                         int32_t num_kv_heads, int32_t head_dim, int32_t block_size, float scale,
+                         void* workspace, int64_t workspace_bytes, void* stream) {
+  PrefillArgs a;
+  int64_t rows = 0;
+  const int bad = prefill_args(&a, &rows, out, out_dtype, out_stride_tok, out_stride_h, q,
+                               q_stride_tok, q_stride_h, k_cache, v_cache, kv_dtype,
+                               kv_stride_slot, kv_stride_head, num_slots, block_tables,
+                               table_stride, max_blocks, context_lens, cu_seqlens_q, n_chunks,
+                               max_query_len, num_heads, num_kv_heads, head_dim, block_size,
+                               scale, 1, nullptr, nullptr);
+  if (bad) return bad == 1 ? 0 : bad;
+  if (workspace_bytes < 0 || (workspace_bytes > 0 && !workspace)) return PKV_E_WORKSPACE;
+  if (workspace && !aligned16(workspace)) return PKV_E_ALIGN;
+  if (workspace && v16_shapes(kv_dtype, head_dim, max_blocks, block_size, num_slots)) {
+    const V16Layout l = v16_layout(head_dim, num_kv_heads, n_chunks, max_blocks, block_size);
+    if (workspace_bytes >= l.total) {
+      a.v16_k = static_cast<const uint8_t*>(workspace);
+      a.v16_kstride = (int32_t)l.kstride;
+      a.v16 = static_cast<const char*>(workspace) + l.k_bytes;
+    }
   }
-  return (int)(kv_dtype == PKV_BF16 ? launch_prefill<PKV_BF16>(a, head_dim, rows, st)
-                                    : launch_prefill<PKV_F16>(a, head_dim, rows, st));
+  return run_prefill(a, rows, kv_dtype, head_dim, max_query_len, (hipStream_t)stream);
 }
 
 }  // extern "C"

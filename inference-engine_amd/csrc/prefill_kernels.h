@@ -28,7 +28,26 @@ struct PrefillArgs {
   int32_t causal;         // 0: every query of chunk c sees all its n_c keys
   const int32_t* q_rows;  // [tokens] or null: query token t reads q row q_rows[t]
   float* lse;             // [tokens, nh] or null: log2 of each softmax's normaliser
+  // bf16 caches: an fp16 copy of each chunk's V (null: none; the kernel with the copy is
+  // launched only with one). Token t of chunk c, KV head h, is row (c * nkv + h) * PM + t,
+  // PM = max_blocks * bs rounded up to kV16Rows, for t below the chunk's clamped context
+  // rounded up to kV16Rows (rows past the context are zero); rows of head_dim fp16
+  // values. Tile i (tokens i kV16Rows ..) of part (c, h) holds V * 2^-k with k =
+  // v16_k[(c * nkv + h) * v16_kstride + i] (0 unless some |V| of the tile is 2^16 or
+  // more), so every value fits fp16.
+  const void* v16;
+  const uint8_t* v16_k;
+  int32_t v16_kstride;
 };
+
+// Tokens per region tile of the fp16 V copy (one workgroup of the copy kernel, one scale
+// exponent); regions are padded to a multiple of it.
+constexpr int kV16Rows = 256;
+// Longest context the copy takes: a wave holds one chunk's scale exponents, four per lane.
+constexpr int kV16MaxTokens = kV16Rows * 4 * kWave;
+__host__ __device__ __forceinline__ int v16_pad(int n) {
+  return (n + kV16Rows - 1) / kV16Rows * kV16Rows;
+}
 
 }  // namespace pkv
 
@@ -256,21 +275,37 @@ template <int HD> struct PrefillShape {
   }
 };
 
-// One work item (chunk, 128-row block, KV head) on a workgroup of 512 threads. Every
-// exit is workgroup-uniform except half 1's after the merge; a caller that runs several
-// items on one workgroup puts a barrier between them (the merge reuses the rings).
-template <int DT, int HD, bool POW2>
-__device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int item) {
+// Coordinates of a work item: chunk c (query rows q0 .. q1 - 1, n context tokens), its
+// 128-row block rbi and KV head kvh.
+struct PrefillItem {
+  int c, q0, q1, n, kvh, rbi;
+};
+
+// The K/V rings of an item: ring[half][0 = K, 1 = V][stage] holds each key half's K and V
+// tiles, two stages each; idring the block-table windows, per half and wave, in a ring
+// of three (one per tile in flight).
+template <int HD> struct PrefillLds {
+  u32x4 ring[2][2][2][PrefillShape<HD>::TILE];
+  int32_t idring[2][3][4][kWave];
+};
+
+// One work item on a workgroup of 512 threads. V16: P.V in fp16 with V from the fp16
+// copy. Every exit is workgroup-uniform except half 1's after the merge; a caller that
+// runs several items on one workgroup puts a barrier between them (the merge reuses the
+// rings).
+template <int DT, int HD, bool POW2, bool V16>
+__device__ __forceinline__ void prefill_body(const PrefillArgs& a, const PrefillItem& it,
+                                             PrefillLds<HD>& lds) {
   using SH = PrefillShape<HD>;
   constexpr int RT = SH::RT, BM = SH::BM, KT = SH::KT, CH = SH::CH, NBETA = SH::NBETA;
   constexpr int NSG = SH::NSG, KS = SH::KS, DTL = SH::DTL, NLD = SH::NLD, TILE = SH::TILE;
   static_assert(HD % 32 == 0 && HD <= 256, "head_dim must be 32..256, a multiple of 32");
-  using MMA = Mfma16x16x32Bits<DT>;
+  static_assert(!V16 || DT == PKV_BF16, "the fp16 V copy serves bf16 caches");
+  using MMA = Mfma16x16x32Bits<DT>;                   // Q.K^T
+  using PM = Mfma16x16x32Bits<V16 ? PKV_F16 : DT>;    // P.V and the row sums
   using S = typename Elt<DT>::S;
-  // ring[half][0 = K, 1 = V][stage]: each key half's K and V tiles, two stages each.
-  __shared__ __align__(16) u32x4 ring[2][2][2][TILE];
-  // Block-table windows, per half and wave, in a ring of three (one per tile in flight).
-  __shared__ __align__(16) int32_t idring[2][3][4][kWave];
+  auto& ring = lds.ring;
+  auto& idring = lds.idring;
 
   const int tid = threadIdx.x;
   const int half = __builtin_amdgcn_readfirstlane(tid >> 8);  // which half of the key tiles
@@ -278,36 +313,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(htid / kWave);  // rows 32 wave .. (RT = 2)
   const int col = lane & 15, grp = lane >> 4;
-  // Work items (chunk, row block, KV head), heaviest first: chunks by context length
-  // (longest first), then row blocks from the last (it sees the most keys), KV heads
-  // innermost. One workgroup fills a CU, so a grid larger than the GPU runs the items
-  // in this order as CUs free up: the longest start earliest.
-  const int kvh = item % a.nkv;
-  const int rbi = (item / a.nkv) % a.row_blocks;
-  const int crank = item / (a.nkv * a.row_blocks);
-  // Each wave ranks up to 63 chunks by itself; larger batches keep their order. Lane j
-  // fetches chunk j's length and query offset (and lane n_chunks the end offset) in one
-  // round trip, so the chunk's numbers come from the lanes, not a second dependent load.
-  const int cap = a.max_blocks * a.bs;
-  int c = crank, q0, q1, n;
-  if (a.n_chunks < kWave) {
-    const int mine = lane < a.n_chunks ? min(max(a.ctx[lane], 0), cap) : -1;
-    const int cq = lane <= a.n_chunks ? a.cu_q[lane] : 0;
-    int rank = 0;
-    for (int j = 0; j < a.n_chunks; ++j) {
-      const int other = __shfl(mine, j);
-      rank += (other > mine) || (other == mine && j < lane);
-    }
-    const uint64_t hit = __ballot(lane < a.n_chunks && rank == crank);
-    c = __builtin_ctzll(hit);
-    q0 = __builtin_amdgcn_readlane(cq, c);
-    q1 = __builtin_amdgcn_readlane(cq, c + 1);  // c + 1 <= n_chunks < 64
-    n = __builtin_amdgcn_readlane(mine, c);
-  } else {
-    q0 = a.cu_q[c];
-    q1 = a.cu_q[c + 1];
-    n = min(max(a.ctx[c], 0), cap);
-  }
+  const int c = it.c, q0 = it.q0, q1 = it.q1, n = it.n, kvh = it.kvh, rbi = it.rbi;
   const int qlen = q1 - q0;
   const int G = a.groups;
   const int nrows = qlen * G;
@@ -336,6 +342,15 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
                   (int64_t)(kvh * G + rr % G) * a.q_sh + 8 * grp;
 #pragma unroll
     for (int s = 0; s < KS; ++s) qf[t][s] = *reinterpret_cast<const u32x4*>(qp + 32 * s);
+  }
+  // V16: the scale exponents of this chunk's KV head part, four per lane (byte i of lane
+  // l: region tile 4 l + i); O^T (d < DTL) then holds the outputs times 2^-kcur.
+  uint32_t kwin = 0;
+  int kcur = 0;
+  if constexpr (V16) {
+    const int kt16 = v16_pad(n) / kV16Rows;
+    const uint8_t* kp = a.v16_k + ((int64_t)c * a.nkv + kvh) * a.v16_kstride;
+    kwin = 4 * lane < kt16 ? *reinterpret_cast<const uint32_t*>(kp + 4 * lane) : 0u;
   }
   // A row block of padding only (every q_rows entry negative: a fixed-shape layout's
   // spare rows) leaves before any key tile; the test is workgroup-uniform.
@@ -425,8 +440,28 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
       dma16_to_lds_s(base + (uint64_t)bid * blk_bytes32, lane_off[r], dst + (uint32_t)(r * 256 * 16));
     }
   };
+  // V16: local tile m's V rows from the chunk's fp16 copy, rows j KT .. j KT + KT - 1 of
+  // this KV head's part of the region (zeros past the context, so no clamping), with the
+  // same granule layout in LDS as the pool's rows.
+  const char* const v16_head =
+      V16 ? reinterpret_cast<const char*>(a.v16) +
+                ((int64_t)c * a.nkv + kvh) * v16_pad(a.max_blocks * a.bs) * (HD * 2)
+          : nullptr;
+  auto issue_v16 = [&](int m) __attribute__((always_inline)) {
+    const int j = gtile(m);
+    const uint32_t dst = ring_lds + (uint32_t)(((2 + (m & 1)) * TILE) * 16);
+    const char* base = v16_head + (int64_t)j * (KT * HD * 2);
+#pragma unroll
+    for (int r = 0; r < NLD; ++r)
+      dma16_to_lds_s(base, (uint32_t)(tok_of(r) * (HD * 2) + chk_of(r) * 16),
+                     dst + (uint32_t)(r * 256 * 16));
+  };
   // K (kv = 0) or V (kv = 1) of local tile m into stage m % 2.
   auto issue_tile = [&](int m, int kv) __attribute__((always_inline)) {
+    if (V16 && kv) {
+      issue_v16(m);
+      return;
+    }
     const int j = gtile(m);
     const int32_t* ids = &idring[half][m % 3][wave][0];
     const int b0 = blk_of(j * KT);
@@ -495,7 +530,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
   // P^T fragment by an all-ones V^T fragment too, so every lane of row n's column holds
   // row n's sum of the same (hi + lo) weights O carries -- no VALU adds, no cross-lane sum.
   f32x4 o[RT][DTL + 1];
-  const u32x4 ones = {MMA::kOnePair, MMA::kOnePair, MMA::kOnePair, MMA::kOnePair};
+  const u32x4 ones = {PM::kOnePair, PM::kOnePair, PM::kOnePair, PM::kOnePair};
 #pragma unroll
   for (int t = 0; t < RT; ++t) {
     m_run[t] = -INFINITY;
@@ -503,6 +538,23 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
 #pragma unroll
     for (int d = 0; d <= DTL; ++d) o[t][d] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
+
+  // V16: O^T (d < DTL, not the row sums) from scale 2^-kcur to 2^-k (a power of two,
+  // exact); uniform, and a no-op unless a tile of the copy was scaled down.
+  auto v16_rescale = [&](int k) __attribute__((always_inline)) {
+    if (k == kcur) return;
+    const float f = __builtin_amdgcn_ldexpf(1.f, kcur - k);
+#pragma unroll
+    for (int t = 0; t < RT; ++t)
+#pragma unroll
+      for (int d = 0; d < DTL; ++d) o[t][d] *= f;
+    kcur = k;
+  };
+  // Before the P.V of local tile m: its region tile's exponent.
+  auto v16_tile_scale = [&](int m) __attribute__((always_inline)) {
+    const int ri = gtile(m) * KT / kV16Rows;
+    v16_rescale((int)((__builtin_amdgcn_readlane(kwin, ri >> 2) >> (8 * (ri & 3))) & 0xFFu));
+  };
 
   // Rows whose causal limit a tile can cross: tile j needs the mask only if it reaches
   // past the smallest limit among this workgroup's rows (its first row's).
@@ -567,6 +619,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
   // step packs its operand fragments here, in the matrix phase, whose VALU is otherwise
   // idle (the softmax phase is the longer one).
   auto pv = [&](int m) __attribute__((always_inline)) {
+    if constexpr (V16) v16_tile_scale(m);
     const char* vstage = reinterpret_cast<const char*>(&ring[half][1][m & 1][0]);
     const int l = fresh_lane();
 #pragma unroll
@@ -585,7 +638,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
           float p8[8];
 #pragma unroll
           for (int e = 0; e < 8; ++e) p8[e] = sc[t][2 * sg + e / 4][e % 4];
-          MMA::pack8(p8, phi[t], plo[t]);
+          PM::pack8(p8, phi[t], plo[t]);
         }
       }
 #pragma unroll
@@ -602,14 +655,14 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
         }
 #pragma unroll
         for (int t = 0; t < RT; ++t) {
-          o[t][d] = MMA::mma(vf, phi[t], o[t][d]);
-          if constexpr (MMA::kSplit) o[t][d] = MMA::mma(vf, plo[t], o[t][d]);
+          o[t][d] = PM::mma(vf, phi[t], o[t][d]);
+          if constexpr (PM::kSplit) o[t][d] = PM::mma(vf, plo[t], o[t][d]);
         }
       }
 #pragma unroll
       for (int t = 0; t < RT; ++t) {  // the row sums
-        o[t][DTL] = MMA::mma(ones, phi[t], o[t][DTL]);
-        if constexpr (MMA::kSplit) o[t][DTL] = MMA::mma(ones, plo[t], o[t][DTL]);
+        o[t][DTL] = PM::mma(ones, phi[t], o[t][DTL]);
+        if constexpr (PM::kSplit) o[t][DTL] = PM::mma(ones, plo[t], o[t][DTL]);
       }
     }
   };
@@ -624,6 +677,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
   constexpr int PIPE = PKV_PREFILL_PIPE > 0 ? PKV_PREFILL_PIPE : 1;
   constexpr int NV = NSG * DTL, NK = NBETA * KS;
   auto pv_qk = [&](int mp, int mq) __attribute__((always_inline)) {
+    if constexpr (V16) v16_tile_scale(mp);
     const char* vstage = reinterpret_cast<const char*>(&ring[half][1][mp & 1][0]);
     const char* kstage = reinterpret_cast<const char*>(&ring[half][0][mq & 1][0]);
     const int l = fresh_lane();
@@ -642,7 +696,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
         float p8[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) p8[e] = sc[t][2 * sg + e / 4][e % 4];
-        MMA::pack8(p8, phi[sg][t], plo[sg][t]);
+        PM::pack8(p8, phi[sg][t], plo[sg][t]);
       }
     // fragment i: V^T (sg, d) = (i / DTL, i % DTL) for i < NV, else K (beta, s)
     auto read_frag = [&](int i) __attribute__((always_inline)) {
@@ -669,14 +723,14 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
         const int sg = i / DTL, d = i % DTL;
 #pragma unroll
         for (int t = 0; t < RT; ++t) {
-          o[t][d] = MMA::mma(f, phi[sg][t], o[t][d]);
-          if constexpr (MMA::kSplit) o[t][d] = MMA::mma(f, plo[sg][t], o[t][d]);
+          o[t][d] = PM::mma(f, phi[sg][t], o[t][d]);
+          if constexpr (PM::kSplit) o[t][d] = PM::mma(f, plo[sg][t], o[t][d]);
         }
         if (d == DTL - 1)
 #pragma unroll
           for (int t = 0; t < RT; ++t) {  // the row sums
-            o[t][DTL] = MMA::mma(ones, phi[sg][t], o[t][DTL]);
-            if constexpr (MMA::kSplit) o[t][DTL] = MMA::mma(ones, plo[sg][t], o[t][DTL]);
+            o[t][DTL] = PM::mma(ones, phi[sg][t], o[t][DTL]);
+            if constexpr (PM::kSplit) o[t][DTL] = PM::mma(ones, plo[sg][t], o[t][DTL]);
           }
       } else {
         const int beta = (i - NV) / KS, s = (i - NV) % KS;
@@ -701,11 +755,11 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
   // second copy would double).
   auto softmax = [&](int j, bool masked) __attribute__((always_inline)) {
     const int kt0 = j * KT;
-    // p = exp2(scale_log2 * s - m_run + kPLog2). The reference m_run is raised only when a
-    // score exceeds it by more than 2^8: a stale reference changes nothing in O / l (both
-    // carry the same factor), keeps p <= 2^(8 + kPLog2), and leaves O untouched on most
-    // tiles. The row
-    // tiles are independent chains: maxima first, one rescale branch, then every exp.
+    // p = exp2(scale_log2 * s - m_run + kPLog2) (kPLog2 of the P.V type). The reference
+    // m_run is raised only when a score exceeds it by more than 2^8: a stale reference
+    // changes nothing in O / l (both carry the same factor), keeps p <= 2^(8 + kPLog2),
+    // and leaves O untouched on most tiles. The row tiles are independent chains: maxima
+    // first, one rescale branch, then every exp.
     float mx[RT];
     bool raise[RT];
     bool any = false;
@@ -735,7 +789,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
         // half's tiles can all lie past a row's causal limit).
         const float alpha = raise[t] ? __builtin_amdgcn_exp2f(m_run[t] - mx[t]) : 1.f;
         m_run[t] = raise[t] ? mx[t] : m_run[t];
-        nref[t] = raise[t] ? MMA::kPLog2 - mx[t] : nref[t];  // a raise sets a finite maximum
+        nref[t] = raise[t] ? PM::kPLog2 - mx[t] : nref[t];  // a raise sets a finite maximum
 #pragma unroll
         for (int d = 0; d <= DTL; ++d) o[t][d] *= alpha;
       }
@@ -755,7 +809,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
 #pragma unroll
         for (int e = 0; e < 8; ++e) p8[e] = sc[t][2 * sg + e / 4][e % 4];
         u32x4 hi, lo;
-        MMA::pack8(p8, hi, lo);
+        PM::pack8(p8, hi, lo);
         sc[t][2 * sg] = __builtin_bit_cast(f32x4, hi);
         sc[t][2 * sg + 1] = __builtin_bit_cast(f32x4, lo);
       }
@@ -813,10 +867,16 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
     issue_ids(m + 3);
 #if PKV_PREFILL_IDS2
     if (POW2 && fast && CH == 16 && NLD == 4 && a.bs_shift == 4 && (gtile(m + 2) + 1) * KT <= n) {
-      const i32x4_a4 v1 = sid4(blk_of(gtile(m + 1) * KT));
-      const i32x4_a4 v2 = sid4(blk_of(gtile(m + 2) * KT));
-      issue_fast(m + 1, 1, v1);
-      issue_fast(m + 2, 0, v2);
+      if constexpr (V16) {  // V from the copy: no block ids
+        const i32x4_a4 v2 = sid4(blk_of(gtile(m + 2) * KT));
+        issue_v16(m + 1);
+        issue_fast(m + 2, 0, v2);
+      } else {
+        const i32x4_a4 v1 = sid4(blk_of(gtile(m + 1) * KT));
+        const i32x4_a4 v2 = sid4(blk_of(gtile(m + 2) * KT));
+        issue_fast(m + 1, 1, v1);
+        issue_fast(m + 2, 0, v2);
+      }
     } else {
       issue_tile(m + 1, 1);
       issue_tile(m + 2, 0);
@@ -869,6 +929,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
   // The last VALU phases issued loads nothing waited for (past the half's end, into
   // free stages); they must land before the rings are reused.
   wait_vmcnt<0>();
+  if constexpr (V16) v16_rescale(0);  // O^T back to the values' own scale
   __syncthreads();
   if (half) {
 #pragma unroll
@@ -910,7 +971,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
     const int rho = rho0 + 16 * RT * wave + 16 * t + col;
     if (a.lse && grp == 0)  // log2 normaliser: the exponent reference m_run plus log2(sum)
       a.lse[(int64_t)(q0 + rho / G) * a.nh + kvh * G + rho % G] =
-          l_tot > 0.f ? m_run[t] + (__log2f(l_tot) - MMA::kPLog2) : -INFINITY;
+          l_tot > 0.f ? m_run[t] + (__log2f(l_tot) - PM::kPLog2) : -INFINITY;
     const int64_t e0 = (int64_t)(q0 + rho / G) * a.out_st + (int64_t)(kvh * G + rho % G) * a.out_sh;
 #pragma unroll
     for (int d = 0; d < DTL; ++d) {
@@ -926,10 +987,132 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int ite
     }
   }
 }
-template <int DT, int HD, bool POW2>
+
+// One work item (chunk, 128-row block, KV head) on a workgroup of 512 threads. Every
+// exit is workgroup-uniform except half 1's after the merge; a caller that runs several
+// items on one workgroup puts a barrier between them (the merge reuses the rings).
+// V16: V from the fp16 copy (bf16 caches; the launch guarantees every chunk's region).
+template <int DT, int HD, bool POW2, bool V16 = false>
+__device__ __forceinline__ void prefill_item(const PrefillArgs& a, const int item) {
+  __shared__ __align__(16) PrefillLds<HD> lds;
+  const int lane = threadIdx.x & (kWave - 1);
+  // Work items (chunk, row block, KV head), heaviest first: chunks by context length
+  // (longest first), then row blocks from the last (it sees the most keys), KV heads
+  // innermost. One workgroup fills a CU, so a grid larger than the GPU runs the items
+  // in this order as CUs free up: the longest start earliest.
+  PrefillItem it;
+  it.kvh = item % a.nkv;
+  it.rbi = (item / a.nkv) % a.row_blocks;
+  const int crank = item / (a.nkv * a.row_blocks);
+  // Each wave ranks up to 63 chunks by itself; larger batches keep their order. Lane j
+  // fetches chunk j's length and query offset (and lane n_chunks the end offset) in one
+  // round trip, so the chunk's numbers come from the lanes, not a second dependent load.
+  const int cap = a.max_blocks * a.bs;
+  it.c = crank;
+  if (a.n_chunks < kWave) {
+    const int mine = lane < a.n_chunks ? min(max(a.ctx[lane], 0), cap) : -1;
+    const int cq = lane <= a.n_chunks ? a.cu_q[lane] : 0;
+    int rank = 0;
+    for (int j = 0; j < a.n_chunks; ++j) {
+      const int other = __shfl(mine, j);
+      rank += (other > mine) || (other == mine && j < lane);
+    }
+    const uint64_t hit = __ballot(lane < a.n_chunks && rank == crank);
+    it.c = __builtin_ctzll(hit);
+    it.q0 = __builtin_amdgcn_readlane(cq, it.c);
+    it.q1 = __builtin_amdgcn_readlane(cq, it.c + 1);  // c + 1 <= n_chunks < 64
+    it.n = __builtin_amdgcn_readlane(mine, it.c);
+  } else {
+    it.q0 = a.cu_q[it.c];
+    it.q1 = a.cu_q[it.c + 1];
+    it.n = min(max(a.ctx[it.c], 0), cap);
+  }
+  prefill_body<DT, HD, POW2, V16>(a, it, lds);
+}
+
+template <int DT, int HD, bool POW2, bool V16>
 __global__ void __launch_bounds__(512)
 paged_prefill_kernel(const PrefillArgs a) {
-  prefill_item<DT, HD, POW2>(a, (int)blockIdx.x);
+  prefill_item<DT, HD, POW2, V16>(a, (int)blockIdx.x);
+}
+
+// The fp16 copy of the chunks' V for the bf16 matrix-core prefill (PrefillArgs::v16):
+// workgroup (i, h, c) converts tokens i kV16Rows .. i kV16Rows + kV16Rows - 1 of chunk
+// c's KV head h (zeros past the context) and writes the tile's scale exponent k: the
+// largest finite |V| of the tile is below 2^(16 + k), so V * 2^-k lies below 2^16, where
+// the largest bf16 value is 65280 and the conversion cannot overflow. bf16 -> fp16 is
+// exact for scaled values of fp16's normal range (2^-14 up); smaller ones round to
+// fp16's subnormal spacing, 2^-24 (times 2^k). Infinities and NaNs stay what they are.
+template <int HD>
+__global__ void __launch_bounds__(256)
+prefill_v16_kernel(const PrefillArgs a) {
+  constexpr int GPR = HD / 8;  // 16-byte granules per row
+  constexpr int PER = kV16Rows * GPR / 256;
+  static_assert(PER >= 1 && kV16Rows * GPR % 256 == 0 && kV16Rows == 256,
+                "one thread per token of the tile, granules split over 256 threads");
+  __shared__ int slots[kV16Rows];
+  __shared__ uint32_t wmax[4];
+  const int i = (int)blockIdx.x, h = (int)blockIdx.y, c = (int)blockIdx.z;
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int cap = a.max_blocks * a.bs;
+  const int tok0 = i * kV16Rows;
+  // One memory trip: the chunk's length and the tile's block ids (every token up to the
+  // table's width; those past the context are not used).
+  const int t = tok0 + (int)threadIdx.x;
+  const int blk = a.bs_shift >= 0 ? (t >> a.bs_shift) : t / a.bs;
+  const int bid = t < cap ? a.tables[(int64_t)c * a.table_stride + blk] : 0;
+  const int n = min(max(a.ctx[c], 0), cap);
+  if (tok0 >= v16_pad(n)) return;  // uniform
+  {  // the tile's slots (block ids outside the pool read slot 0)
+    int sl = -1;
+    if (t < n) {
+      const int64_t s64 = (int64_t)bid * a.bs + (t - blk * a.bs);
+      sl = (s64 >= 0 && s64 < a.num_slots) ? (int)s64 : 0;  // num_slots < 2^31 (launch)
+    }
+    slots[threadIdx.x] = sl;
+  }
+  __syncthreads();
+  const char* vsrc = reinterpret_cast<const char*>(a.v) + (int64_t)h * a.kv_sh * 2;
+  u32x4 x[PER];
+  uint32_t emax = 0;  // largest biased exponent of a finite value
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int g = k * 256 + (int)threadIdx.x;
+    const int sl = slots[g / GPR];
+    x[k] = sl >= 0 ? *reinterpret_cast<const u32x4*>(vsrc + ((int64_t)sl * a.kv_ss + (g % GPR) * 8) * 2)
+                   : u32x4{0u, 0u, 0u, 0u};
+  }
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const uint32_t w[4] = {x[k].x, x[k].y, x[k].z, x[k].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t e0 = (w[e] >> 7) & 0xFFu, e1 = (w[e] >> 23) & 0xFFu;
+      emax = max(emax, max(e0 == 0xFFu ? 0u : e0, e1 == 0xFFu ? 0u : e1));
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) emax = max(emax, (uint32_t)__shfl_xor((int)emax, off));
+  if (lane == 0) wmax[wave] = emax;
+  __syncthreads();
+  emax = max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3]));
+  const int ks = max(0, (int)emax - 127 - 15);  // |V| < 2^(emax - 126)
+  const float f = __builtin_amdgcn_ldexpf(1.f, -ks);
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  char* dst = reinterpret_cast<char*>(const_cast<void*>(a.v16)) +
+              (((int64_t)c * a.nkv + h) * v16_pad(cap) + tok0) * (HD * 2);
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int g = k * 256 + (int)threadIdx.x;
+    uint32_t w[4] = {x[k].x, x[k].y, x[k].z, x[k].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      w[e] = __builtin_bit_cast(uint32_t, h2{(_Float16)(__uint_as_float(w[e] << 16) * f),
+                                             (_Float16)(__uint_as_float(w[e] & 0xFFFF0000u) * f)});
+    *reinterpret_cast<u32x4*>(dst + (int64_t)g * 16) = u32x4{w[0], w[1], w[2], w[3]};
+  }
+  if (threadIdx.x == 0)
+    const_cast<uint8_t*>(a.v16_k)[((int64_t)c * a.nkv + h) * a.v16_kstride + i] = (uint8_t)ks;
 }
 
 }  // namespace

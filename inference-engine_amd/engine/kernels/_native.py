@@ -18,7 +18,7 @@ LIB_PATH = os.path.join(
     "lib",
     "libpaged_kv.so",
 )
-ABI_VERSION = 4
+ABI_VERSION = 5
 PKV_NOALLOC_SCRATCH_BYTES = 32 << 20  # include/paged_kv.h
 
 PKV_F32, PKV_F16, PKV_BF16 = 0, 1, 2
@@ -109,6 +109,17 @@ SIGNATURES: dict[str, tuple] = {
          _p, _i64, _i32,                          # block tables
          _p, _p, _i32, _i32,                      # ctx, cu_q, n_chunks, max_query_len
          _i32, _i32, _i32, _i32, _f32, _p],       # nh, nkv, hd, bs, scale, stream
+    ),  # fmt: skip
+    "pkv_prefill_workspace_bytes": (_i64, [ctypes.c_int, _i32, _i32, _i32, _i32, _i32]),
+    "pkv_paged_prefill_ws": (
+        ctypes.c_int,
+        [_p, ctypes.c_int, _i64, _i64,            # out
+         _p, _i64, _i64,                          # q
+         _p, _p, ctypes.c_int, _i64, _i64, _i64,  # k, v caches
+         _p, _i64, _i32,                          # block tables
+         _p, _p, _i32, _i32,                      # ctx, cu_q, n_chunks, max_query_len
+         _i32, _i32, _i32, _i32, _f32,            # nh, nkv, hd, bs, scale
+         _p, _i64, _p],                           # workspace, bytes, stream
     ),  # fmt: skip
 }
 

@@ -577,6 +577,7 @@ def paged_prefill_attention(
     max_query_len: int,
     *,
     out: torch.Tensor | None = None,
+    workspace: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Bottom-right causal attention of prompt chunks over the paged pool.
 
@@ -593,7 +594,13 @@ def paged_prefill_attention(
     16-bit caches at head_dim 32-256 run on the matrix cores (the reference's
     FlashAttention shapes); fp32 caches and head_dim 16 (the reference's per-chunk SDPA
     path, layers.py:254-265) on a VALU kernel that stages each K/V tile in LDS once per
-    16 query tokens.
+    16 query tokens. For bf16 caches the call first writes each chunk's V as fp16 (per
+    256-token tile scaled by a power of two that keeps it inside fp16's range) into a
+    workspace, so that P enters the second product once, in fp16, instead of as a bf16
+    hi + lo pair; ``workspace`` (a CUDA byte tensor of at least
+    ``prefill_workspace_bytes(...)``) supplies it, else the call allocates one of that
+    size through torch (at most ``PREFILL_WORKSPACE_MAX_BYTES``; beyond it, and for other
+    dtypes, the call takes no copy).
     """
     what = "paged_prefill_attention"
     dev = _native.require_gpu(what, q, k_cache, v_cache, block_tables, context_lens,
@@ -634,17 +641,43 @@ def paged_prefill_attention(
                       cu_seqlens_q, t, max_query_len)  # fmt: skip
     context_lens = context_lens.contiguous()
     cu_seqlens_q = cu_seqlens_q.contiguous()
-    status = _native.lib().pkv_paged_prefill(
+    kv_code = _native.dtype_code(k_cache.dtype, what)
+    if workspace is None:
+        need = prefill_workspace_bytes(k_cache.dtype, hd, nkv, n_chunks, block_tables.shape[1],
+                                       block_size)  # fmt: skip
+        if 0 < need <= PREFILL_WORKSPACE_MAX_BYTES:
+            workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    elif not workspace.is_contiguous() or workspace.device != dev:
+        raise ValueError(f"{what}: workspace must be a contiguous tensor on {dev}")
+    ws_ptr = workspace.data_ptr() if workspace is not None else None
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    status = _native.lib().pkv_paged_prefill_ws(
         out.data_ptr(), _native.dtype_code(out.dtype, what), out.stride(0), out.stride(1),
         q.data_ptr(), q.stride(0), q.stride(1),
-        k_cache.data_ptr(), v_cache.data_ptr(), _native.dtype_code(k_cache.dtype, what),
+        k_cache.data_ptr(), v_cache.data_ptr(), kv_code,
         k_cache.stride(0), k_cache.stride(1), k_cache.shape[0],
         block_tables.data_ptr(), block_tables.stride(0), block_tables.shape[1],
         context_lens.data_ptr(), cu_seqlens_q.data_ptr(), n_chunks, int(max_query_len),
-        nh, nkv, hd, block_size, hd**-0.5, _native.stream_of(dev),
+        nh, nkv, hd, block_size, hd**-0.5, ws_ptr, ws_bytes, _native.stream_of(dev),
     )  # fmt: skip
     _native.check(status, what)
     return out
+
+
+# Largest workspace paged_prefill_attention allocates by itself for the fp16 V copy.
+PREFILL_WORKSPACE_MAX_BYTES = 1 << 30
+
+
+def prefill_workspace_bytes(dtype: torch.dtype, head_dim: int, num_kv_heads: int,
+                            n_chunks: int, max_blocks: int, block_size: int) -> int:
+    """Workspace bytes with which a prefill call of these static shapes writes the fp16
+    copy of every chunk's V (0: the shapes take none; pkv_prefill_workspace_bytes)."""
+    n = _native.lib().pkv_prefill_workspace_bytes(
+        _native.DTYPE_CODE.get(dtype, -1), head_dim, num_kv_heads, n_chunks, max_blocks,
+        block_size)  # fmt: skip
+    if n < 0:
+        _native.check(n, "prefill_workspace_bytes")
+    return int(n)
 
 
 def _check_chunks(what, block_tables, context_lens, block_size, num_slots, cu_seqlens_q,

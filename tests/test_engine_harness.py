@@ -208,7 +208,11 @@ def test_engine_kernels_match_static_loop_fp32(budget):
 def test_engine_kernels_match_reference_backend_16bit(dtype, hd, bs):
     """16-bit: decode kernel + MFMA chunked-prefill kernel against the same engine on the
     reference's gather-then-attention (fp32 math, rounded to the model dtype), on the
-    same flattened steps: identical tokens, logits within rounding."""
+    same flattened steps: identical tokens, logits within rounding. A sequence may part
+    only at a step where the reference's own two best logits lie within that rounding
+    tolerance of each other (a 16-bit tie, which any other order of rounding can break
+    the other way; this bf16 model has one, at a gap of exactly 0); it is compared up to
+    there. The fp32 engine tests above admit no such exception."""
     from tiny_llama import KernelBackend
 
     model = _cuda_model(dtype, hidden_size=4 * hd, num_attention_heads=4,
@@ -218,11 +222,22 @@ def test_engine_kernels_match_reference_backend_16bit(dtype, hd, bs):
         eng = TinyEngine(model, backend, num_blocks=64, block_size=bs,
                          max_num_batched_tokens=8)  # fmt: skip
         runs[backend.name] = (_run_staggered(eng, PROMPTS, 10), eng)
-    assert runs["kernel"][0] == runs["reference"][0]
-    worst = max((torch.stack(runs["kernel"][1].logits[r]) -
-                 torch.stack(runs["reference"][1].logits[r])).abs().max().item()
-                for r in PROMPTS)  # fmt: skip
-    assert worst <= 0.05, worst  # 16-bit activations: a few ulps of the logits
+    atol = 0.05  # 16-bit activations: a few ulps of the logits
+    worst, parted = 0.0, []
+    for r in PROMPTS:
+        got, want = runs["kernel"][0][r], runs["reference"][0][r]
+        assert len(got) == len(want), r
+        for i, (tg, tw) in enumerate(zip(got, want)):
+            lg = runs["kernel"][1].logits[r][i].float()
+            lw = runs["reference"][1].logits[r][i].float()
+            worst = max(worst, (lg - lw).abs().max().item())
+            if tg != tw:
+                top = torch.topk(lw, 2).values
+                assert (top[0] - top[1]).item() <= atol, (r, i, tg, tw, top.tolist())
+                parted.append((r, i))
+                break
+    assert worst <= atol, worst
+    assert len(parted) <= 1, parted
 
 
 @pytest.mark.gpu

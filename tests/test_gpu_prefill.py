@@ -313,3 +313,103 @@ def test_prefill_fp16_tiny_weights_keep_their_mass():
     assert want > 7e-3
     err = (got[0] - want).abs().max().item()
     assert err < 2e-4, err
+
+
+def _prefill_c_abi(entry, q, k, v, tables, ctx, cu, bs, max_q, workspace=None):
+    """One call of pkv_paged_prefill (entry "plain") or pkv_paged_prefill_ws ("ws", with
+    ``workspace``: None = none) through the C ABI; fp32 output on the CPU."""
+    from engine.kernels import _native
+
+    nh, hd = q.shape[1], q.shape[2]
+    nkv = k.shape[1]
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    td, cd, cud = tables.to(DEV), ctx.to(DEV), cu.to(DEV)
+    out = torch.full(q.shape, float("nan"), dtype=torch.float32, device=DEV)
+    args = [out.data_ptr(), _native.PKV_F32, out.stride(0), out.stride(1), qd.data_ptr(),
+            qd.stride(0), qd.stride(1), kd.data_ptr(), vd.data_ptr(), _native.dtype_code(q.dtype, "t"),
+            kd.stride(0), kd.stride(1), kd.shape[0], td.data_ptr(), td.stride(0), td.shape[1],
+            cd.data_ptr(), cud.data_ptr(), len(ctx), max_q, nh, nkv, hd, bs, hd**-0.5]  # fmt: skip
+    stream = torch.cuda.current_stream().cuda_stream
+    if entry == "plain":
+        st = _native.lib().pkv_paged_prefill(*args, stream)
+    else:
+        ws = workspace
+        st = _native.lib().pkv_paged_prefill_ws(
+            *args, ws.data_ptr() if ws is not None else None,
+            ws.numel() if ws is not None else 0, stream)  # fmt: skip
+    _native.check(st, entry)
+    torch.cuda.synchronize()
+    return out.cpu()
+
+
+@pytest.mark.parametrize(("nh", "nkv", "hd", "bs"),
+                         [(32, 8, 128, 16), (8, 2, 64, 12), (4, 1, 256, 16), (6, 2, 32, 1),
+                          (16, 2, 128, 32), (12, 4, 64, 16)])  # fmt: skip
+def test_prefill_bf16_fp16_copy_of_v(nh, nkv, hd, bs):
+    """bf16 caches through pkv_paged_prefill_ws: each chunk's V copied to fp16 once per
+    call, P multiplied once in fp16. Within 2e-3 of the oracle, like the bf16 hi + lo
+    product of pkv_paged_prefill on the same inputs; contexts across several 256-token
+    tiles of the copy, empty and one-token chunks, block sizes that are not powers of two."""
+    _say("prefill fp16 V copy", nh, nkv, hd, bs)
+    spec = [(37, 700), (1, 1), (0, 5), (64, 64), (100, 1030), (16, 300)]
+    q, k, v, tables, ctx, cu = _chunks(spec, nh, nkv, hd, bs, torch.bfloat16, seed=hd + bs + nh)
+    need = pa.prefill_workspace_bytes(torch.bfloat16, hd, nkv, len(spec), tables.shape[1], bs)
+    assert need > 0
+    ws = torch.empty(need, dtype=torch.uint8, device=DEV)
+    ws.fill_(0xFF)  # scratch: whatever it held before must not matter
+    got = _prefill_c_abi("ws", q, k, v, tables, ctx, cu, bs, 100, ws)
+    hilo = _prefill_c_abi("plain", q, k, v, tables, ctx, cu, bs, 100)
+    want = oracle.prefill_attention(q, k, v, tables, cu, ctx, bs, threads=THREADS)
+    assert (got - want).abs().max().item() <= ATOL
+    assert (hilo - want).abs().max().item() <= ATOL
+    # the same call again on the dirty workspace: the same bits
+    again = _prefill_c_abi("ws", q, k, v, tables, ctx, cu, bs, 100, ws)
+    assert torch.equal(got, again)
+
+
+def test_prefill_workspace_too_small_is_the_plain_call():
+    """A workspace below pkv_prefill_workspace_bytes (or none) runs the bf16 hi + lo
+    kernel: bit for bit the output of pkv_paged_prefill."""
+    _say("prefill small workspace")
+    bs, nh, nkv, hd = 16, 8, 2, 128
+    spec = [(20, 400), (5, 90)]
+    q, k, v, tables, ctx, cu = _chunks(spec, nh, nkv, hd, bs, torch.bfloat16, seed=21)
+    need = pa.prefill_workspace_bytes(torch.bfloat16, hd, nkv, len(spec), tables.shape[1], bs)
+    plain = _prefill_c_abi("plain", q, k, v, tables, ctx, cu, bs, 20)
+    short = torch.empty(need - 16, dtype=torch.uint8, device=DEV)
+    assert torch.equal(_prefill_c_abi("ws", q, k, v, tables, ctx, cu, bs, 20, short), plain)
+    assert torch.equal(_prefill_c_abi("ws", q, k, v, tables, ctx, cu, bs, 20, None), plain)
+    # fp16 caches and tables past 65,536 tokens take no copy: workspace size 0
+    assert pa.prefill_workspace_bytes(torch.float16, hd, nkv, 2, 32, bs) == 0
+    assert pa.prefill_workspace_bytes(torch.bfloat16, hd, nkv, 2, 4097, bs) == 0
+    assert pa.prefill_workspace_bytes(torch.bfloat16, hd, nkv, 2, 4096, bs) > 0
+
+
+def test_prefill_fp16_copy_scales_tiles_beyond_fp16():
+    """Tiles of the fp16 V copy whose |V| reaches 2^16 are stored times 2^-k and the
+    matrix-core kernel rescales its accumulators between tiles of different k: chunk 0
+    has a 256-token tile of values near 3e5 between ordinary ones, chunk 1 starts with
+    values near -2e5 and goes on with ordinary ones, chunk 2 is ordinary. Each chunk
+    within 2e-3 of the oracle relative to the largest |V| it reads."""
+    _say("prefill fp16 copy scaled tiles")
+    bs, nh, nkv, hd = 16, 8, 2, 128
+    spec = [(30, 1000), (40, 700), (20, 300)]
+    q, k, v, tables, ctx, cu = _chunks(spec, nh, nkv, hd, bs, torch.bfloat16, seed=22)
+
+    def rows_of(c, t0, t1):
+        pos = torch.arange(t0, t1)
+        return tables[c, pos // bs].long() * bs + pos % bs
+
+    big0, big1 = rows_of(0, 256, 512), rows_of(1, 0, 100)
+    v[big0] = (v[big0].float() * 3e5).to(torch.bfloat16)
+    v[big1] = (v[big1].float() * -2e5).to(torch.bfloat16)
+    need = pa.prefill_workspace_bytes(torch.bfloat16, hd, nkv, len(spec), tables.shape[1], bs)
+    ws = torch.empty(need, dtype=torch.uint8, device=DEV)
+    got = _prefill_c_abi("ws", q, k, v, tables, ctx, cu, bs, 40, ws)
+    want = oracle.prefill_attention(q, k, v, tables, cu, ctx, bs, threads=THREADS)
+    assert torch.isfinite(got).all()
+    for c, rows in enumerate((big0, big1, None)):
+        lo, hi = int(cu[c]), int(cu[c + 1])
+        scale = max(1.0, v[rows].float().abs().max().item()) if rows is not None else 1.0
+        err = (got[lo:hi] - want[lo:hi]).abs().max().item()
+        assert err <= ATOL * scale, (c, err, scale)
