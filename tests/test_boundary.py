@@ -82,6 +82,48 @@ def test_workspace_arithmetic():
         assert lib.pkv_decode_default_workgroups(2, 128, 24, 8, 8, 32, 16) == -6
 
 
+def test_prefill_workspace_arithmetic():
+    """pkv_prefill_workspace_bytes: one scale byte per 256-token tile of every (chunk, KV
+    head) (rows of a multiple of 4 bytes, the area rounded up to 256), then every
+    chunk's region at the table's width rounded up to 256 tokens, fp16; 0 for shapes
+    that take no copy; PKV_E_SHAPE for bad ones. Host arithmetic only (no GPU)."""
+    lib = _native.lib()
+    # bf16 (2), hd 128, 8 KV heads, 4 chunks, 224 blocks of 16 = 3,584 tokens -> 3,584
+    kstride = (3584 // 256 + 3) // 4 * 4
+    k_area = (4 * 8 * kstride + 255) // 256 * 256
+    assert lib.pkv_prefill_workspace_bytes(2, 128, 8, 4, 224, 16) == k_area + 4 * 3584 * 8 * 128 * 2
+    # widths round up to 256 tokens: 10 blocks of 12 = 120 tokens -> 256
+    k_area = (3 * 2 * 4 + 255) // 256 * 256
+    assert lib.pkv_prefill_workspace_bytes(2, 64, 2, 3, 10, 12) == k_area + 3 * 256 * 2 * 64 * 2
+    assert lib.pkv_prefill_workspace_bytes(2, 128, 8, 0, 224, 16) == 0  # no chunks
+    assert lib.pkv_prefill_workspace_bytes(1, 128, 8, 4, 224, 16) == 0  # fp16 caches
+    assert lib.pkv_prefill_workspace_bytes(0, 128, 8, 4, 224, 16) == 0  # fp32 caches
+    assert lib.pkv_prefill_workspace_bytes(2, 16, 8, 4, 224, 16) == 0   # hd 16: VALU kernel
+    assert lib.pkv_prefill_workspace_bytes(2, 128, 8, 4, 4097, 16) == 0  # past 65,536 tokens
+    assert lib.pkv_prefill_workspace_bytes(2, 128, 8, 4, 4096, 16) > 0
+    assert lib.pkv_prefill_workspace_bytes(2, 128, 0, 4, 224, 16) == -2
+    assert lib.pkv_prefill_workspace_bytes(2, 128, 8, 4, 224, 0) == -2
+    assert lib.pkv_prefill_workspace_bytes(2, 128, 8, -1, 224, 16) == -2
+    assert pa.prefill_workspace_bytes(torch.bfloat16, 128, 8, 4, 224, 16) > 0
+    with pytest.raises(ValueError):
+        pa.prefill_workspace_bytes(torch.bfloat16, 128, 8, 4, 224, 0)
+
+
+def test_prefill_ws_rejects_before_launch():
+    """pkv_paged_prefill_ws checks the workspace after the common prefill arguments:
+    negative bytes, or bytes without a pointer -> PKV_E_WORKSPACE; a workspace not
+    16-byte aligned -> PKV_E_ALIGN; no chunks -> success with nothing launched."""
+    lib = _native.lib()
+    base = [1 << 12, 2, 8 * 128, 128, 1 << 12, 8 * 128, 128, 1 << 12, 1 << 12, 2, 2 * 128,
+            128, 64, 1 << 12, 4, 4, 1 << 12, 1 << 12, 1, 4, 8, 2, 128, 16, 0.088]  # fmt: skip
+    assert lib.pkv_paged_prefill_ws(*base, None, -1, None) == -4
+    assert lib.pkv_paged_prefill_ws(*base, None, 4096, None) == -4
+    assert lib.pkv_paged_prefill_ws(*base, (1 << 12) + 4, 4096, None) == -3
+    empty = list(base)
+    empty[18] = 0  # n_chunks
+    assert lib.pkv_paged_prefill_ws(*empty, None, 0, None) == 0
+
+
 def _decode_args(**over):
     a = dict(out=1 << 12, out_dtype=2, osb=24 * 128, osh=128, q=1 << 12, qsb=24 * 128,
              qsh=128, k=1 << 12, v=1 << 12, kv_dtype=2, kss=1024, ksh=128, num_slots=64,
