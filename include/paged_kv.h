@@ -304,7 +304,7 @@ int pkv_paged_prefill_ex(void* out, int out_dtype, int64_t out_stride_tok, int64
  * shapes: about n_chunks x (max_blocks * block_size rounded up to 256) x num_kv_heads x
  * head_dim x 2, plus one scale byte per 256 tokens of each. 0 for shapes that take no
  * copy (fp16 or fp32 caches, head_dim 16, tables of more than 65,536 tokens); negative:
- * PKV_E_SHAPE. No counterpart in the reference (whose varlen path
+ * PKV_E_DTYPE or PKV_E_SHAPE. No counterpart in the reference (whose varlen path
  * gathers each chunk's K and V into new tensors itself).
  */
 int64_t pkv_prefill_workspace_bytes(int kv_dtype, int32_t head_dim, int32_t num_kv_heads,

@@ -440,7 +440,10 @@ int pkv_paged_prefill_ex(void* out, int out_dtype, int64_t out_stride_tok, int64
 
 int64_t pkv_prefill_workspace_bytes(int kv_dtype, int32_t head_dim, int32_t num_kv_heads,
                                     int32_t n_chunks, int32_t max_blocks, int32_t block_size) {
-  if (num_kv_heads <= 0 || n_chunks < 0 || max_blocks < 0 || block_size <= 0 ||
+  if (!valid_dtype(kv_dtype)) return PKV_E_DTYPE;
+  if (!(head_dim == 16 || head_dim == 32 || head_dim == 64 || head_dim == 128 ||
+        head_dim == 256) ||
+      num_kv_heads <= 0 || n_chunks < 0 || max_blocks < 0 || block_size <= 0 ||
       (int64_t)max_blocks * block_size > (int64_t)1 << 30)
     return PKV_E_SHAPE;
   if (!v16_shapes(kv_dtype, head_dim, max_blocks, block_size, 0)) return 0;

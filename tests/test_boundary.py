@@ -101,6 +101,8 @@ def test_prefill_workspace_arithmetic():
     assert lib.pkv_prefill_workspace_bytes(2, 16, 8, 4, 224, 16) == 0   # hd 16: VALU kernel
     assert lib.pkv_prefill_workspace_bytes(2, 128, 8, 4, 4097, 16) == 0  # past 65,536 tokens
     assert lib.pkv_prefill_workspace_bytes(2, 128, 8, 4, 4096, 16) > 0
+    assert lib.pkv_prefill_workspace_bytes(7, 128, 8, 4, 224, 16) == -1  # no such dtype
+    assert lib.pkv_prefill_workspace_bytes(2, 96, 8, 4, 224, 16) == -2
     assert lib.pkv_prefill_workspace_bytes(2, 128, 0, 4, 224, 16) == -2
     assert lib.pkv_prefill_workspace_bytes(2, 128, 8, 4, 224, 0) == -2
     assert lib.pkv_prefill_workspace_bytes(2, 128, 8, -1, 224, 16) == -2
