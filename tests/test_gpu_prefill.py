@@ -413,3 +413,66 @@ def test_prefill_fp16_copy_scales_tiles_beyond_fp16():
         scale = max(1.0, v[rows].float().abs().max().item()) if rows is not None else 1.0
         err = (got[lo:hi] - want[lo:hi]).abs().max().item()
         assert err <= ATOL * scale, (c, err, scale)
+
+
+@pytest.mark.parametrize("workspace", ["inside", "given"])
+def test_prefill_fp16_copy_under_graph_replay(workspace):
+    """The two-dispatch bf16 prefill call (fp16 copy of V, then the matrix-core kernel)
+    captured in a hipGraph: its workspace allocated inside the capture (from the graph's
+    pool) or passed in. Three replays with new queries, new K/V, new block tables and
+    context lengths (within the captured table width), eager work and synchronisations
+    between them; every replay bit-equal to the eager call and within 2e-3 of the oracle."""
+    _say("prefill fp16 copy graph", workspace)
+    bs, nh, nkv, hd, width, max_q = 16, 8, 2, 128, 40, 48
+    n_chunks = 3
+    nblk = n_chunks * width + 4
+    k_pool = torch.zeros(nblk * bs, nkv, hd, dtype=torch.bfloat16, device=DEV)
+    v_pool = torch.zeros_like(k_pool)
+    q_s = torch.zeros(n_chunks * max_q, nh, hd, dtype=torch.bfloat16, device=DEV)
+    tables_s = torch.zeros(n_chunks, width, dtype=torch.int32, device=DEV)
+    ctx_s = torch.ones(n_chunks, dtype=torch.int32, device=DEV)
+    cu_s = torch.zeros(n_chunks + 1, dtype=torch.int32, device=DEV)
+    out_s = torch.empty(q_s.shape, dtype=torch.float32, device=DEV)
+    ws = None
+    if workspace == "given":
+        need = pa.prefill_workspace_bytes(torch.bfloat16, hd, nkv, n_chunks, width, bs)
+        ws = torch.empty(need, dtype=torch.uint8, device=DEV)
+
+    def body():
+        pa.paged_prefill_attention(q_s, k_pool, v_pool, tables_s, ctx_s, bs, cu_s, max_q,
+                                   out=out_s, workspace=ws)  # fmt: skip
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        body()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        body()
+
+    for rep in range(3):
+        g = torch.Generator().manual_seed(200 + rep)
+        qlen = torch.randint(0, max_q + 1, (n_chunks,), generator=g)
+        ctx = torch.clamp(qlen + torch.randint(0, width * bs - max_q, (n_chunks,), generator=g),
+                          max=width * bs)  # fmt: skip
+        cu = torch.zeros(n_chunks + 1, dtype=torch.int32)
+        cu[1:] = qlen.cumsum(0).int()
+        q_s.copy_(torch.randn(q_s.shape, generator=g).to(torch.bfloat16))
+        k_pool.copy_(torch.randn(k_pool.shape, generator=g).to(torch.bfloat16))
+        v_pool.copy_(torch.randn(v_pool.shape, generator=g).to(torch.bfloat16))
+        tables_s.copy_(torch.randperm(nblk, generator=g)[: n_chunks * width].view(n_chunks, width).int())
+        ctx_s.copy_(ctx.int())
+        cu_s.copy_(cu)
+        graph.replay()
+        torch.cuda.synchronize()
+        got = out_s.clone()
+        want = torch.empty_like(out_s)
+        pa.paged_prefill_attention(q_s, k_pool, v_pool, tables_s, ctx_s, bs, cu_s, max_q,
+                                   out=want)  # fmt: skip
+        torch.cuda.synchronize()
+        rows = int(cu[-1])
+        assert torch.equal(got[:rows], want[:rows]), f"replay {rep}"
+        ref = oracle.prefill_attention(q_s[:rows].cpu(), k_pool.cpu(), v_pool.cpu(),
+                                       tables_s.cpu(), cu, ctx_s.cpu(), bs, threads=THREADS)
+        assert (got[:rows].cpu() - ref).abs().max().item() <= ATOL, f"replay {rep}"
