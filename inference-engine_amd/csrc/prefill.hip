@@ -238,12 +238,15 @@ hipError_t launch_prefill(const PrefillArgs& a, int hd, int64_t rows, hipStream_
   }
 }
 
-// The fp16 V copy ahead of a bf16 matrix-core prefill: grid (region tiles of the widest
-// possible context, KV heads, chunks); workgroups past their chunk's context leave.
+// The fp16 V copy ahead of a bf16 matrix-core prefill: one workgroup per (region tile of
+// the widest possible context, KV head, chunk), KV head innermost; workgroups past their
+// chunk's context leave.
 hipError_t launch_v16(const PrefillArgs& a, int hd, hipStream_t st) {
   const int64_t tiles = ((int64_t)a.max_blocks * a.bs + kV16Rows - 1) / kV16Rows;
-  if (tiles < 1) return hipSuccess;
-  const dim3 grid((unsigned)tiles, (unsigned)a.nkv, (unsigned)a.n_chunks), block(256);
+  const int64_t wgs = tiles * a.nkv * a.n_chunks;
+  if (wgs < 1) return hipSuccess;
+  if (wgs > 0x7FFFFFFF) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)wgs), block(256);
   switch (hd) {
     case 32: hipLaunchKernelGGL((prefill_v16_kernel<32>), grid, block, 0, st, a); break;
     case 64: hipLaunchKernelGGL((prefill_v16_kernel<64>), grid, block, 0, st, a); break;

@@ -1037,8 +1037,9 @@ paged_prefill_kernel(const PrefillArgs a) {
 }
 
 // The fp16 copy of the chunks' V for the bf16 matrix-core prefill (PrefillArgs::v16):
-// workgroup (i, h, c) converts tokens i kV16Rows .. i kV16Rows + kV16Rows - 1 of chunk
-// c's KV head h (zeros past the context) and writes the tile's scale exponent k: the
+// workgroup h + nkv (i + T c) (T tiles per chunk at the table's width) converts tokens
+// i kV16Rows .. i kV16Rows + kV16Rows - 1 of chunk c's KV head h (zeros past the
+// context) and writes the tile's scale exponent k: the
 // largest finite |V| of the tile is below 2^(16 + k), so V * 2^-k lies below 2^16, where
 // the largest bf16 value is 65280 and the conversion cannot overflow. bf16 -> fp16 is
 // exact for scaled values of fp16's normal range (2^-14 up); smaller ones round to
@@ -1052,9 +1053,15 @@ prefill_v16_kernel(const PrefillArgs a) {
                 "one thread per token of the tile, granules split over 256 threads");
   __shared__ int slots[kV16Rows];
   __shared__ uint32_t wmax[4];
-  const int i = (int)blockIdx.x, h = (int)blockIdx.y, c = (int)blockIdx.z;
-  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  // KV head innermost: workgroups are dealt to the XCDs round-robin, so with a multiple
+  // of 8 KV heads head h's copy is written from XCD h mod 8, as the prefill's work items
+  // of head h run there.
   const int cap = a.max_blocks * a.bs;
+  const int tiles = (cap + kV16Rows - 1) / kV16Rows;
+  const int h = (int)(blockIdx.x % (unsigned)a.nkv);
+  const int rest = (int)(blockIdx.x / (unsigned)a.nkv);
+  const int i = rest % tiles, c = rest / tiles;
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
   const int tok0 = i * kV16Rows;
   // One memory trip: the chunk's length and the tile's block ids (every token up to the
   // table's width; those past the context are not used).
@@ -1109,7 +1116,10 @@ prefill_v16_kernel(const PrefillArgs a) {
     for (int e = 0; e < 4; ++e)
       w[e] = __builtin_bit_cast(uint32_t, h2{(_Float16)(__uint_as_float(w[e] << 16) * f),
                                              (_Float16)(__uint_as_float(w[e] & 0xFFFF0000u) * f)});
-    *reinterpret_cast<u32x4*>(dst + (int64_t)g * 16) = u32x4{w[0], w[1], w[2], w[3]};
+    // streaming stores: the copy is not kept dirty in this XCD's L2 (no write-back at
+    // the kernel's end); the prefill reads it once per XCD, then from its own L2
+    __builtin_nontemporal_store(u32x4{w[0], w[1], w[2], w[3]},
+                                reinterpret_cast<u32x4*>(dst + (int64_t)g * 16));
   }
   if (threadIdx.x == 0)
     const_cast<uint8_t*>(a.v16_k)[((int64_t)c * a.nkv + h) * a.v16_kstride + i] = (uint8_t)ks;
