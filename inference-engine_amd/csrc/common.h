@@ -56,9 +56,6 @@ constexpr int kWave = 64;
 #ifndef PKV_CASCADE_TAIL_EIGHTHS
 #define PKV_CASCADE_TAIL_EIGHTHS 2
 #endif
-#ifndef PKV_PREFILL_SETPRIO
-#define PKV_PREFILL_SETPRIO 0
-#endif
 #ifndef PKV_PREFILL_SWZ
 #define PKV_PREFILL_SWZ 1
 #endif

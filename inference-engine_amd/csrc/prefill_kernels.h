@@ -77,6 +77,12 @@ __host__ __device__ __forceinline__ int v16_pad(int n) {
 #ifndef PKV_PREFILL_VALU_PRIO
 #define PKV_PREFILL_VALU_PRIO 0
 #endif
+// 1: the matrix-core prefill raises a wave's priority for its matrix phases (measured
+// with the fp16 P.V: 80.1-80.2 against 81.1-81.6 µs per config-5 call, config 3's
+// cascade unchanged; with the bf16 hi + lo product it had cost 2%); 0: no priorities.
+#ifndef PKV_PREFILL_SETPRIO
+#define PKV_PREFILL_SETPRIO 1
+#endif
 
 namespace {
 
