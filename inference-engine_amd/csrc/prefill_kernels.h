@@ -833,7 +833,18 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const Prefill
   // but the loads of the previous VALU phase (2 NLD + 1), before each VALU phase for
   // all but that phase's K and V loads (its block ids must be in). Loads complete in
   // issue order.
-  if (nt > 0) {  // prologue: block ids of tiles 0-2, K of 0 and 1, V of 0
+  // V from the fp16 copy and both first K tiles inside 16-token blocks: their block ids
+  // come in one scalar trip, V0 (no ids) goes out before it returns, and K1 goes out
+  // last, so the first matrix phase waits for V0 and K0 only (one trip fewer before it).
+  const bool pro2 = PKV_PREFILL_IDS2 && V16 && POW2 && fast && CH == 16 && NLD == 4 &&
+                    a.bs_shift == 4 && nt > 0 && (gtile(1) + 1) * KT <= n;
+  if (pro2) {
+    const i32x4_a4 v0 = sid4(blk_of(gtile(0) * KT));
+    const i32x4_a4 v1 = sid4(blk_of(gtile(1) * KT));
+    issue_v16(0);
+    issue_fast(0, 0, v0);
+    issue_fast(1, 0, v1);
+  } else if (nt > 0) {  // prologue: block ids of tiles 0-2, K of 0 and 1, V of 0
     if (!seg_uniform) {  // the LDS ring's ids must land first; scalar-loaded ids need not
       issue_ids(0);      // wait for the query loads still in flight
       issue_ids(1);
@@ -856,6 +867,8 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const Prefill
       // all but the previous VALU phase's loads: K and V (and the ids, through the LDS)
       if (seg_uniform) wait_vmcnt<2 * NLD>();
       else wait_vmcnt<2 * NLD + 1>();
+    } else if (m == 0 && pro2) {
+      wait_vmcnt<NLD>();  // all but K1
     } else {
       wait_vmcnt<0>();
     }
