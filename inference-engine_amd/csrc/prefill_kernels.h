@@ -446,6 +446,30 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const Prefill
       dma16_to_lds_s(base + (uint64_t)bid * blk_bytes32, lane_off[r], dst + (uint32_t)(r * 256 * 16));
     }
   };
+  // 16-token blocks at head_dim 128 (a tile is four blocks, a half four waves; callers
+  // check the block size and that the tile lies inside the context): wave w loads block
+  // w of the tile, its four DMAs (tokens 4 r .. 4 r + 3 of the block) from one base. The
+  // tile's LDS layout is the one above; only which wave fills which granules differs
+  // (wave w: granules 256 w .. 256 w + 255), so each wave needs one block id and one
+  // address per tile, not four.
+  constexpr bool kBlockWave = CH == 16 && NLD == 4 && KT == 64;
+  uint32_t lane_offb[NLD];
+#pragma unroll
+  for (int r = 0; r < NLD; ++r) {
+    const int t = 4 * r + lane / CH;  // token inside the block (and its low 4 bits in the tile)
+    lane_offb[r] = (uint32_t)((t * a.kv_ss + ((lane % CH) ^ SH::swz(t)) * 8) * (int64_t)sizeof(S));
+  }
+  const uint32_t ring_lds_bw = lds_addr(&ring[half][0][0][0]) + (uint32_t)(wave * NLD * kWave * 16);
+  // This wave's block id of local tile m (a scalar load; the tile is inside the context).
+  auto wave_id = [&](int m) { return sid(blk_of(gtile(m) * KT) + wave); };
+  auto issue_block = [&](int m, int kv, int id) __attribute__((always_inline)) {
+    const uint32_t dst = ring_lds_bw + (uint32_t)(((kv * 2 + (m & 1)) * TILE) * 16);
+    uint32_t bid = (uint32_t)id;
+    bid = bid < pool_blocks ? bid : 0u;  // memory safety only
+    const char* base = kv_base[kv] + (uint64_t)bid * blk_bytes32;
+#pragma unroll
+    for (int r = 0; r < NLD; ++r) dma16_to_lds_s(base, lane_offb[r], dst + (uint32_t)(r * kWave * 16));
+  };
   // V16: local tile m's V rows from the chunk's fp16 copy, rows j KT .. j KT + KT - 1 of
   // this KV head's part of the region (zeros past the context, so no clamping), with the
   // same granule layout in LDS as the pool's rows.
@@ -836,14 +860,13 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const Prefill
   // V from the fp16 copy and both first K tiles inside 16-token blocks: their block ids
   // come in one scalar trip, V0 (no ids) goes out before it returns, and K1 goes out
   // last, so the first matrix phase waits for V0 and K0 only (one trip fewer before it).
-  const bool pro2 = PKV_PREFILL_IDS2 && V16 && POW2 && fast && CH == 16 && NLD == 4 &&
-                    a.bs_shift == 4 && nt > 0 && (gtile(1) + 1) * KT <= n;
+  const bool pro2 = PKV_PREFILL_IDS2 && V16 && kBlockWave && POW2 && fast && a.bs_shift == 4 &&
+                    nt > 0 && (gtile(1) + 1) * KT <= n;
   if (pro2) {
-    const i32x4_a4 v0 = sid4(blk_of(gtile(0) * KT));
-    const i32x4_a4 v1 = sid4(blk_of(gtile(1) * KT));
+    const int k0 = wave_id(0), k1 = wave_id(1);
     issue_v16(0);
-    issue_fast(0, 0, v0);
-    issue_fast(1, 0, v1);
+    issue_block(0, 0, k0);
+    issue_block(1, 0, k1);
   } else if (nt > 0) {  // prologue: block ids of tiles 0-2, K of 0 and 1, V of 0
     if (!seg_uniform) {  // the LDS ring's ids must land first; scalar-loaded ids need not
       issue_ids(0);      // wait for the query loads still in flight
@@ -885,16 +908,15 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const Prefill
 #endif
     issue_ids(m + 3);
 #if PKV_PREFILL_IDS2
-    if (POW2 && fast && CH == 16 && NLD == 4 && a.bs_shift == 4 && (gtile(m + 2) + 1) * KT <= n) {
+    if (kBlockWave && POW2 && fast && a.bs_shift == 4 && (gtile(m + 2) + 1) * KT <= n) {
       if constexpr (V16) {  // V from the copy: no block ids
-        const i32x4_a4 v2 = sid4(blk_of(gtile(m + 2) * KT));
+        const int k2 = wave_id(m + 2);
         issue_v16(m + 1);
-        issue_fast(m + 2, 0, v2);
+        issue_block(m + 2, 0, k2);
       } else {
-        const i32x4_a4 v1 = sid4(blk_of(gtile(m + 1) * KT));
-        const i32x4_a4 v2 = sid4(blk_of(gtile(m + 2) * KT));
-        issue_fast(m + 1, 1, v1);
-        issue_fast(m + 2, 0, v2);
+        const int v1 = wave_id(m + 1), k2 = wave_id(m + 2);
+        issue_block(m + 1, 1, v1);
+        issue_block(m + 2, 0, k2);
       }
     } else {
       issue_tile(m + 1, 1);
