@@ -29,12 +29,15 @@ struct PrefillArgs {
   const int32_t* q_rows;  // [tokens] or null: query token t reads q row q_rows[t]
   float* lse;             // [tokens, nh] or null: log2 of each softmax's normaliser
   // bf16 caches: an fp16 copy of each chunk's V (null: none; the kernel with the copy is
-  // launched only with one). Token t of chunk c, KV head h, is row (c * nkv + h) * PM + t,
-  // PM = max_blocks * bs rounded up to kV16Rows, for t below the chunk's clamped context
-  // rounded up to kV16Rows (rows past the context are zero); rows of head_dim fp16
-  // values. Tile i (tokens i kV16Rows ..) of part (c, h) holds V * 2^-k with k =
-  // v16_k[(c * nkv + h) * v16_kstride + i] (0 unless some |V| of the tile is 2^16 or
-  // more), so every value fits fp16.
+  // launched only with one). Part (c, h) (chunk c, KV head h) starts at token slot
+  // (c * nkv + h) * PM, PM = max_blocks * bs rounded up to kV16Rows, a slot being
+  // head_dim fp16 values, and covers the chunk's clamped context rounded up to kV16Rows
+  // (tokens past the context are zero). Each KT-token tile of the prefill (PrefillShape)
+  // is stored in V^T operand order, not by rows: its fragment (32-key step sg, 16-dim
+  // tile d) is 1 KiB, lane l's 16 bytes (dims 16 d + l % 16 of the tile's keys 32 sg +
+  // 16 (e / 4) + 4 (l / 16) + e % 4, e = 0 .. 7) at l * 16. Region tile i (tokens i
+  // kV16Rows ..) of part (c, h) holds V * 2^-k with k = v16_k[(c * nkv + h) * v16_kstride
+  // + i] (0 unless some |V| of the tile is 2^16 or more), so every value fits fp16.
   const void* v16;
   const uint8_t* v16_k;
   int32_t v16_kstride;
@@ -279,7 +282,37 @@ template <int HD> struct PrefillShape {
 #endif
     else return t % CH;
   }
+  // LDS byte offset (inside a 32-key step of a tile) of lane l's V^T transpose read:
+  // lane (col, grp) reads key 16 h2 + 4 grp + col / 4, dims 16 d + 4 (col % 4) .. +4
+  // (chunk 2 d + (col % 4) / 2, half (col % 4) & 1); h2 > 0 only when rows have more
+  // than 16 chunks.
+  __device__ static uint32_t voff(int l, int h2, int d) {
+    const int c4 = l & 3, tr = 4 * (l >> 4) + ((l & 15) >> 2);
+    const int tk = 16 * h2 + tr;
+    return (uint32_t)((((2 * d + c4 / 2) ^ swz(tk)) * 16 + (c4 & 1) * 8) + tr * CH * 16);
+  }
 };
+
+// The V^T operand fragment (32-key step sg, 16-dim tile d) of a V tile held in LDS in the
+// swizzled row layout: two ds_read_b64_tr_b16 transpose reads per lane. Lane (col, grp)
+// gets dims 16 d + col of keys 32 sg + 16 (e / 4) + 4 grp + e % 4, e = 0 .. 7 -- the
+// order in which a lane holds its own probabilities P^T.
+template <int HD>
+__device__ __forceinline__ u32x4 vt_frag_tr(const char* vstage, int l, int sg, int d) {
+  using SH = PrefillShape<HD>;
+  constexpr int CH = SH::CH, VSW = CH > 16 ? 2 : 1;
+  u32x4 f;
+#pragma unroll
+  for (int h2 = 0; h2 < 2; ++h2) {
+    // generic -> LDS address space (an addrspacecast of a __shared__ pointer)
+    const s16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_s16x4*)(vstage + (32 * sg + 16 * h2) * CH * 16 + SH::voff(l, VSW == 1 ? 0 : h2, d)));
+    const uint32_t lo = (uint32_t)(uint16_t)x[0] | ((uint32_t)(uint16_t)x[1] << 16);
+    const uint32_t hi = (uint32_t)(uint16_t)x[2] | ((uint32_t)(uint16_t)x[3] << 16);
+    if (h2 == 0) { f.x = lo; f.y = hi; } else { f.z = lo; f.w = hi; }
+  }
+  return f;
+}
 
 // Coordinates of a work item: chunk c (query rows q0 .. q1 - 1, n context tokens), its
 // 128-row block rbi and KV head kvh.
@@ -470,9 +503,9 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const Prefill
 #pragma unroll
     for (int r = 0; r < NLD; ++r) dma16_to_lds_s(base, lane_offb[r], dst + (uint32_t)(r * kWave * 16));
   };
-  // V16: local tile m's V rows from the chunk's fp16 copy, rows j KT .. j KT + KT - 1 of
-  // this KV head's part of the region (zeros past the context, so no clamping), with the
-  // same granule layout in LDS as the pool's rows.
+  // V16: local tile m's V from the chunk's fp16 copy, tile j of this KV head's part of the
+  // region (zeros past the context, so no clamping), already in operand order: the tile's
+  // granules land in LDS in their own order.
   const char* const v16_head =
       V16 ? reinterpret_cast<const char*>(a.v16) +
                 ((int64_t)c * a.nkv + kvh) * v16_pad(a.max_blocks * a.bs) * (HD * 2)
@@ -483,8 +516,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const Prefill
     const char* base = v16_head + (int64_t)j * (KT * HD * 2);
 #pragma unroll
     for (int r = 0; r < NLD; ++r)
-      dma16_to_lds_s(base, (uint32_t)(tok_of(r) * (HD * 2) + chk_of(r) * 16),
-                     dst + (uint32_t)(r * 256 * 16));
+      dma16_to_lds_s(base + r * 256 * 16, (uint32_t)(htid * 16), dst + (uint32_t)(r * 256 * 16));
   };
   // K (kv = 0) or V (kv = 1) of local tile m into stage m % 2.
   auto issue_tile = [&](int m, int kv) __attribute__((always_inline)) {
@@ -598,10 +630,8 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const Prefill
   // they are used (a few VALU instructions; holding them would cost 12 registers).
   //   K: lane (col, grp) reads key 16 beta + col, chunk 4 s + grp. swz(key) depends on
   //      beta only when a row has more than 16 chunks (head_dim 256).
-  //   V^T: lane (col, grp) reads key 32 sg + 16 h2 + 4 grp + col / 4, dims 16 d +
-  //      4 (col % 4) .. +4 (chunk 2 d + (col % 4) / 2, half (col % 4) & 1).
+  //   V^T: see PrefillShape::voff (pool rows), or one 16-byte read (the fp16 copy).
   constexpr int KSW = CH > 16 ? NBETA : 1;
-  constexpr int VSW = CH > 16 ? 2 : 1;
   auto fresh_lane = [&]() {  // lane, as a value the compiler must not hoist
     int l = lane;
     __asm__ volatile("" : "+v"(l));
@@ -611,10 +641,14 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const Prefill
     const int tk = 16 * b + (l & 15);
     return (uint32_t)(((4 * s + (l >> 4)) ^ SH::swz(tk)) * 16 + (l & 15) * CH * 16);
   };
-  auto voff = [&](int l, int h2, int d) {
-    const int c4 = l & 3, tr = 4 * (l >> 4) + ((l & 15) >> 2);
-    const int tk = 16 * h2 + tr;
-    return (uint32_t)((((2 * d + c4 / 2) ^ SH::swz(tk)) * 16 + (c4 & 1) * 8) + tr * CH * 16);
+  // V^T operand fragment (32-key step sg, 16-dim tile d) of the V tile at vstage. The
+  // fp16 copy stores every tile in operand order (fragment (sg, d) is 1 KiB, lane l's 16
+  // bytes at l * 16), so a fragment is one conflict-free ds_read_b128; V from the pool
+  // takes two transpose reads of the swizzled rows (a timing copy that read V^T with one
+  // 16-byte read per fragment ran 1.5 µs faster per config-5 call).
+  auto vt_frag = [&](const char* vstage, int l, int sg, int d) __attribute__((always_inline)) {
+    if constexpr (V16) return *reinterpret_cast<const u32x4*>(vstage + ((sg * DTL + d) * kWave + l) * 16);
+    else return vt_frag_tr<HD>(vstage, l, sg, d);
   };
 
   // S^T of a tile from its QK^T to its softmax, then in the same registers its
@@ -673,16 +707,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const Prefill
       }
 #pragma unroll
       for (int d = 0; d < DTL; ++d) {
-        u32x4 vf;
-#pragma unroll
-        for (int h2 = 0; h2 < 2; ++h2) {
-          // generic -> LDS address space (an addrspacecast of a __shared__ pointer)
-          const s16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (lds_s16x4*)(vstage + (32 * sg + 16 * h2) * CH * 16 + voff(l, VSW == 1 ? 0 : h2, d)));
-          const uint32_t lo = (uint32_t)(uint16_t)x[0] | ((uint32_t)(uint16_t)x[1] << 16);
-          const uint32_t hi = (uint32_t)(uint16_t)x[2] | ((uint32_t)(uint16_t)x[3] << 16);
-          if (h2 == 0) { vf.x = lo; vf.y = hi; } else { vf.z = lo; vf.w = hi; }
-        }
+        const u32x4 vf = vt_frag(vstage, l, sg, d);
 #pragma unroll
         for (int t = 0; t < RT; ++t) {
           o[t][d] = PM::mma(vf, phi[t], o[t][d]);
@@ -732,15 +757,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const Prefill
     auto read_frag = [&](int i) __attribute__((always_inline)) {
       u32x4 f;
       if (i < NV) {
-        const int sg = i / DTL, d = i % DTL;
-#pragma unroll
-        for (int h2 = 0; h2 < 2; ++h2) {
-          const s16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (lds_s16x4*)(vstage + (32 * sg + 16 * h2) * CH * 16 + voff(l, VSW == 1 ? 0 : h2, d)));
-          const uint32_t lo = (uint32_t)(uint16_t)x[0] | ((uint32_t)(uint16_t)x[1] << 16);
-          const uint32_t hi = (uint32_t)(uint16_t)x[2] | ((uint32_t)(uint16_t)x[3] << 16);
-          if (h2 == 0) { f.x = lo; f.y = hi; } else { f.z = lo; f.w = hi; }
-        }
+        f = vt_frag(vstage, l, i / DTL, i % DTL);
       } else {
         const int beta = (i - NV) / KS, s = (i - NV) % KS;
         f = *reinterpret_cast<const u32x4*>(kstage + beta * 16 * CH * 16 +
@@ -1080,7 +1097,8 @@ paged_prefill_kernel(const PrefillArgs a) {
 // The fp16 copy of the chunks' V for the bf16 matrix-core prefill (PrefillArgs::v16):
 // workgroup h + nkv (i + T c) (T tiles per chunk at the table's width) converts tokens
 // i kV16Rows .. i kV16Rows + kV16Rows - 1 of chunk c's KV head h (zeros past the
-// context) and writes the tile's scale exponent k: the
+// context), stores them in operand order through LDS, and writes the tile's scale
+// exponent k: the
 // largest finite |V| of the tile is below 2^(16 + k), so V * 2^-k lies below 2^16, where
 // the largest bf16 value is 65280 and the conversion cannot overflow. bf16 -> fp16 is
 // exact for scaled values of fp16's normal range (2^-14 up); smaller ones round to
@@ -1092,8 +1110,15 @@ prefill_v16_kernel(const PrefillArgs a) {
   constexpr int PER = kV16Rows * GPR / 256;
   static_assert(PER >= 1 && kV16Rows * GPR % 256 == 0 && kV16Rows == 256,
                 "one thread per token of the tile, granules split over 256 threads");
+  using SH = PrefillShape<HD>;
+  constexpr int KT = SH::KT, NSG = SH::NSG, DTL = SH::DTL;
+  constexpr int TILES = kV16Rows / KT;  // matrix-core prefill tiles per region tile
+  static_assert(GPR == SH::CH && TILES % 4 == 0, "whole prefill tiles per wave");
   __shared__ int slots[kV16Rows];
   __shared__ uint32_t wmax[4];
+  // The converted region tile in the prefill's LDS layout for V rows (granule (token t,
+  // position p) holds chunk p ^ swz(t)), read back as V^T operand fragments.
+  __shared__ __align__(16) u32x4 stage[kV16Rows * GPR];
   // KV head innermost: workgroups are dealt to the XCDs round-robin, so with a multiple
   // of 8 KV heads head h's copy is written from XCD h mod 8, as the prefill's work items
   // of head h run there.
@@ -1157,10 +1182,25 @@ prefill_v16_kernel(const PrefillArgs a) {
     for (int e = 0; e < 4; ++e)
       w[e] = __builtin_bit_cast(uint32_t, h2{(_Float16)(__uint_as_float(w[e] << 16) * f),
                                              (_Float16)(__uint_as_float(w[e] & 0xFFFF0000u) * f)});
-    // streaming stores: the copy is not kept dirty in this XCD's L2 (no write-back at
-    // the kernel's end); the prefill reads it once per XCD, then from its own L2
-    __builtin_nontemporal_store(u32x4{w[0], w[1], w[2], w[3]},
-                                reinterpret_cast<u32x4*>(dst + (int64_t)g * 16));
+    const int t = g / GPR, ch = g % GPR;  // token of the region tile, 16-byte chunk of its row
+    stage[t * GPR + (ch ^ SH::swz(t))] = u32x4{w[0], w[1], w[2], w[3]};
+  }
+  __syncthreads();
+  // Wave w writes prefill tiles w, w + 4, .. of the region tile in operand order:
+  // fragment (sg, d) of a tile is 1 KiB, lane l's 16 bytes at l * 16 (what the prefill
+  // reads with one ds_read_b128). Streaming stores: the copy is not kept dirty in this
+  // XCD's L2 (no write-back at the kernel's end); the prefill reads it once per XCD, then
+  // from its own L2.
+#pragma unroll
+  for (int q = wave; q < TILES; q += 4) {
+    const char* tile = reinterpret_cast<const char*>(&stage[q * KT * GPR]);
+    char* tdst = dst + (int64_t)q * (KT * HD * 2);
+#pragma unroll
+    for (int sg = 0; sg < NSG; ++sg)
+#pragma unroll
+      for (int d = 0; d < DTL; ++d)
+        __builtin_nontemporal_store(vt_frag_tr<HD>(tile, lane, sg, d),
+                                    reinterpret_cast<u32x4*>(tdst + ((sg * DTL + d) * kWave + lane) * 16));
   }
   if (threadIdx.x == 0)
     const_cast<uint8_t*>(a.v16_k)[((int64_t)c * a.nkv + h) * a.v16_kstride + i] = (uint8_t)ks;
