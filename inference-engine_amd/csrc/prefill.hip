@@ -246,7 +246,7 @@ hipError_t launch_v16(const PrefillArgs& a, int hd, hipStream_t st) {
   const int64_t wgs = tiles * a.nkv * a.n_chunks;
   if (wgs < 1) return hipSuccess;
   if (wgs > 0x7FFFFFFF) return hipErrorInvalidValue;
-  const dim3 grid((unsigned)wgs), block(256);
+  const dim3 grid((unsigned)wgs), block(kV16Threads);
   switch (hd) {
     case 32: hipLaunchKernelGGL((prefill_v16_kernel<32>), grid, block, 0, st, a); break;
     case 64: hipLaunchKernelGGL((prefill_v16_kernel<64>), grid, block, 0, st, a); break;

@@ -46,6 +46,8 @@ struct PrefillArgs {
 // Tokens per region tile of the fp16 V copy (one workgroup of the copy kernel, one scale
 // exponent); regions are padded to a multiple of it.
 constexpr int kV16Rows = 256;
+// Threads of a workgroup of the copy (one per region tile).
+constexpr int kV16Threads = 512;
 // Longest context the copy takes: a wave holds one chunk's scale exponents, four per lane.
 constexpr int kV16MaxTokens = kV16Rows * 4 * kWave;
 __host__ __device__ __forceinline__ int v16_pad(int n) {
@@ -85,6 +87,11 @@ __host__ __device__ __forceinline__ int v16_pad(int n) {
 // cascade unchanged; with the bf16 hi + lo product it had cost 2%); 0: no priorities.
 #ifndef PKV_PREFILL_SETPRIO
 #define PKV_PREFILL_SETPRIO 1
+#endif
+// Waves of a half (of 4) that issue their VALU phase's K/V loads after the softmax
+// instead of before it.
+#ifndef PKV_PREFILL_LATE_DMA
+#define PKV_PREFILL_LATE_DMA 2
 #endif
 
 namespace {
@@ -924,26 +931,36 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const Prefill
     __builtin_amdgcn_s_setprio(1);
 #endif
     issue_ids(m + 3);
+    // The phase's K/V loads: V of tile m + 1, K of tile m + 2, both used three phases on.
+    auto loads = [&]() __attribute__((always_inline)) {
 #if PKV_PREFILL_IDS2
-    if (kBlockWave && POW2 && fast && a.bs_shift == 4 && (gtile(m + 2) + 1) * KT <= n) {
-      if constexpr (V16) {  // V from the copy: no block ids
-        const int k2 = wave_id(m + 2);
-        issue_v16(m + 1);
-        issue_block(m + 2, 0, k2);
+      if (kBlockWave && POW2 && fast && a.bs_shift == 4 && (gtile(m + 2) + 1) * KT <= n) {
+        if constexpr (V16) {  // V from the copy: no block ids
+          const int k2 = wave_id(m + 2);
+          issue_v16(m + 1);
+          issue_block(m + 2, 0, k2);
+        } else {
+          const int v1 = wave_id(m + 1), k2 = wave_id(m + 2);
+          issue_block(m + 1, 1, v1);
+          issue_block(m + 2, 0, k2);
+        }
       } else {
-        const int v1 = wave_id(m + 1), k2 = wave_id(m + 2);
-        issue_block(m + 1, 1, v1);
-        issue_block(m + 2, 0, k2);
+        issue_tile(m + 1, 1);
+        issue_tile(m + 2, 0);
       }
-    } else {
+#else
       issue_tile(m + 1, 1);
       issue_tile(m + 2, 0);
-    }
-#else
-    issue_tile(m + 1, 1);
-    issue_tile(m + 2, 0);
 #endif
+    };
+    // The four waves' loads of a phase are 32 DMA instructions of 1 KiB, ~512 cycles of
+    // the CU's address unit (64 bytes a cycle); a wave cannot start its softmax until its
+    // own have been taken. The last PKV_PREFILL_LATE_DMA waves of the half issue theirs
+    // after the softmax, by when the others' have drained.
+    const bool late = wave >= 4 - PKV_PREFILL_LATE_DMA;  // wave-uniform
+    if (!late) loads();
     softmax(tbeg + m, tbeg + m >= j_mask);
+    if (late) loads();
 #if PKV_PREFILL_VALU_PRIO == 1
     __builtin_amdgcn_s_setprio(0);
 #endif
@@ -1104,18 +1121,20 @@ paged_prefill_kernel(const PrefillArgs a) {
 // exact for scaled values of fp16's normal range (2^-14 up); smaller ones round to
 // fp16's subnormal spacing, 2^-24 (times 2^k). Infinities and NaNs stay what they are.
 template <int HD>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(kV16Threads)
 prefill_v16_kernel(const PrefillArgs a) {
+  constexpr int NT = kV16Threads, NW = NT / kWave;
   constexpr int GPR = HD / 8;  // 16-byte granules per row
-  constexpr int PER = kV16Rows * GPR / 256;
-  static_assert(PER >= 1 && kV16Rows * GPR % 256 == 0 && kV16Rows == 256,
-                "one thread per token of the tile, granules split over 256 threads");
+  constexpr int PER = kV16Rows * GPR / NT;
+  static_assert(PER >= 1 && kV16Rows * GPR % NT == 0 && kV16Rows == 256 && NT >= kV16Rows,
+                "granules split evenly over the threads, one thread per token for the ids");
   using SH = PrefillShape<HD>;
   constexpr int KT = SH::KT, NSG = SH::NSG, DTL = SH::DTL;
   constexpr int TILES = kV16Rows / KT;  // matrix-core prefill tiles per region tile
-  static_assert(GPR == SH::CH && TILES % 4 == 0, "whole prefill tiles per wave");
+  constexpr int NFRAG = TILES * NSG * DTL;  // V^T operand fragments per region tile
+  static_assert(GPR == SH::CH, "rows of CH granules");
   __shared__ int slots[kV16Rows];
-  __shared__ uint32_t wmax[4];
+  __shared__ uint32_t wmax[NW];
   // The converted region tile in the prefill's LDS layout for V rows (granule (token t,
   // position p) holds chunk p ^ swz(t)), read back as V^T operand fragments.
   __shared__ __align__(16) u32x4 stage[kV16Rows * GPR];
@@ -1131,12 +1150,13 @@ prefill_v16_kernel(const PrefillArgs a) {
   const int tok0 = i * kV16Rows;
   // One memory trip: the chunk's length and the tile's block ids (every token up to the
   // table's width; those past the context are not used).
+  const bool id_thread = threadIdx.x < kV16Rows;  // thread t: token tok0 + t's id
   const int t = tok0 + (int)threadIdx.x;
   const int blk = a.bs_shift >= 0 ? (t >> a.bs_shift) : t / a.bs;
-  const int bid = t < cap ? a.tables[(int64_t)c * a.table_stride + blk] : 0;
+  const int bid = id_thread && t < cap ? a.tables[(int64_t)c * a.table_stride + blk] : 0;
   const int n = min(max(a.ctx[c], 0), cap);
   if (tok0 >= v16_pad(n)) return;  // uniform
-  {  // the tile's slots (block ids outside the pool read slot 0)
+  if (id_thread) {  // the tile's slots (block ids outside the pool read slot 0)
     int sl = -1;
     if (t < n) {
       const int64_t s64 = (int64_t)bid * a.bs + (t - blk * a.bs);
@@ -1150,7 +1170,7 @@ prefill_v16_kernel(const PrefillArgs a) {
   uint32_t emax = 0;  // largest biased exponent of a finite value
 #pragma unroll
   for (int k = 0; k < PER; ++k) {
-    const int g = k * 256 + (int)threadIdx.x;
+    const int g = k * NT + (int)threadIdx.x;
     const int sl = slots[g / GPR];
     x[k] = sl >= 0 ? *reinterpret_cast<const u32x4*>(vsrc + ((int64_t)sl * a.kv_ss + (g % GPR) * 8) * 2)
                    : u32x4{0u, 0u, 0u, 0u};
@@ -1168,7 +1188,9 @@ prefill_v16_kernel(const PrefillArgs a) {
   for (int off = 32; off >= 1; off >>= 1) emax = max(emax, (uint32_t)__shfl_xor((int)emax, off));
   if (lane == 0) wmax[wave] = emax;
   __syncthreads();
-  emax = max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3]));
+  emax = wmax[0];
+#pragma unroll
+  for (int k = 1; k < NW; ++k) emax = max(emax, wmax[k]);
   const int ks = max(0, (int)emax - 127 - 15);  // |V| < 2^(emax - 126)
   const float f = __builtin_amdgcn_ldexpf(1.f, -ks);
   typedef _Float16 h2 __attribute__((ext_vector_type(2)));
@@ -1176,7 +1198,7 @@ prefill_v16_kernel(const PrefillArgs a) {
               (((int64_t)c * a.nkv + h) * v16_pad(cap) + tok0) * (HD * 2);
 #pragma unroll
   for (int k = 0; k < PER; ++k) {
-    const int g = k * 256 + (int)threadIdx.x;
+    const int g = k * NT + (int)threadIdx.x;
     uint32_t w[4] = {x[k].x, x[k].y, x[k].z, x[k].w};
 #pragma unroll
     for (int e = 0; e < 4; ++e)
@@ -1186,21 +1208,17 @@ prefill_v16_kernel(const PrefillArgs a) {
     stage[t * GPR + (ch ^ SH::swz(t))] = u32x4{w[0], w[1], w[2], w[3]};
   }
   __syncthreads();
-  // Wave w writes prefill tiles w, w + 4, .. of the region tile in operand order:
-  // fragment (sg, d) of a tile is 1 KiB, lane l's 16 bytes at l * 16 (what the prefill
-  // reads with one ds_read_b128). Streaming stores: the copy is not kept dirty in this
-  // XCD's L2 (no write-back at the kernel's end); the prefill reads it once per XCD, then
-  // from its own L2.
+  // The region tile's prefill tiles in operand order: fragment (sg, d) of a tile is 1
+  // KiB, lane l's 16 bytes at l * 16 (what the prefill reads with one ds_read_b128);
+  // wave w writes fragments w, w + NW, .. of the region tile. Streaming stores: the copy
+  // is not kept dirty in this XCD's L2 (no write-back at the kernel's end); the prefill
+  // reads it once per XCD, then from its own L2.
 #pragma unroll
-  for (int q = wave; q < TILES; q += 4) {
+  for (int fi = wave; fi < NFRAG; fi += NW) {
+    const int q = fi / (NSG * DTL), sg = (fi / DTL) % NSG, d = fi % DTL;
     const char* tile = reinterpret_cast<const char*>(&stage[q * KT * GPR]);
-    char* tdst = dst + (int64_t)q * (KT * HD * 2);
-#pragma unroll
-    for (int sg = 0; sg < NSG; ++sg)
-#pragma unroll
-      for (int d = 0; d < DTL; ++d)
-        __builtin_nontemporal_store(vt_frag_tr<HD>(tile, lane, sg, d),
-                                    reinterpret_cast<u32x4*>(tdst + ((sg * DTL + d) * kWave + lane) * 16));
+    __builtin_nontemporal_store(vt_frag_tr<HD>(tile, lane, sg, d),
+                                reinterpret_cast<u32x4*>(dst + (int64_t)fi * (kWave * 16) + lane * 16));
   }
   if (threadIdx.x == 0)
     const_cast<uint8_t*>(a.v16_k)[((int64_t)c * a.nkv + h) * a.v16_kstride + i] = (uint8_t)ks;
