@@ -93,6 +93,17 @@ __host__ __device__ __forceinline__ int v16_pad(int n) {
 #ifndef PKV_PREFILL_LATE_DMA
 #define PKV_PREFILL_LATE_DMA 2
 #endif
+// 1: a wave masks its tile's scores and takes their row maxima at the end of the matrix
+// phase that computed them, not at the start of the softmax phase.
+#ifndef PKV_PREFILL_EARLY_MAX
+#define PKV_PREFILL_EARLY_MAX 1
+#endif
+// 1: the steady-state matrix phase issues QK^T of its tile before P.V of the previous
+// one, so the scores are in when the phase ends and takes their row maxima (measured at
+// config 5: 77.75-77.80 against 77.56-77.64 µs per call for 0, 16 more VGPRs).
+#ifndef PKV_PREFILL_QK_FIRST
+#define PKV_PREFILL_QK_FIRST 0
+#endif
 
 namespace {
 
@@ -760,21 +771,26 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const Prefill
         for (int e = 0; e < 8; ++e) p8[e] = sc[t][2 * sg + e / 4][e % 4];
         PM::pack8(p8, phi[sg][t], plo[sg][t]);
       }
-    // fragment i: V^T (sg, d) = (i / DTL, i % DTL) for i < NV, else K (beta, s)
+    // fragment i: V^T (sg, d) = (iv / DTL, iv % DTL) for a V fragment, K (beta, s) = (ik /
+    // KS, ik % KS) for a K one; K fragments first with PKV_PREFILL_QK_FIRST.
+    constexpr bool QKF = PKV_PREFILL_QK_FIRST;
+    auto is_v = [&](int i) { return QKF ? i >= NK : i < NV; };
+    auto vi = [&](int i) { return QKF ? i - NK : i; };
+    auto ki = [&](int i) { return QKF ? i : i - NV; };
     auto read_frag = [&](int i) __attribute__((always_inline)) {
       u32x4 f;
-      if (i < NV) {
-        f = vt_frag(vstage, l, i / DTL, i % DTL);
+      if (is_v(i)) {
+        f = vt_frag(vstage, l, vi(i) / DTL, vi(i) % DTL);
       } else {
-        const int beta = (i - NV) / KS, s = (i - NV) % KS;
+        const int beta = ki(i) / KS, s = ki(i) % KS;
         f = *reinterpret_cast<const u32x4*>(kstage + beta * 16 * CH * 16 +
                                             koff(l, KSW == 1 ? 0 : beta, s));
       }
       return f;
     };
     auto mma_frag = [&](int i, const u32x4& f) __attribute__((always_inline)) {
-      if (i < NV) {
-        const int sg = i / DTL, d = i % DTL;
+      if (is_v(i)) {
+        const int sg = vi(i) / DTL, d = vi(i) % DTL;
 #pragma unroll
         for (int t = 0; t < RT; ++t) {
           o[t][d] = PM::mma(f, phi[sg][t], o[t][d]);
@@ -787,7 +803,7 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const Prefill
             if constexpr (PM::kSplit) o[t][DTL] = PM::mma(ones, plo[sg][t], o[t][DTL]);
           }
       } else {
-        const int beta = (i - NV) / KS, s = (i - NV) % KS;
+        const int beta = ki(i) / KS, s = ki(i) % KS;
 #pragma unroll
         for (int t = 0; t < RT; ++t)
           sc[t][beta] = MMA::mma(f, qf[t][s], s == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : sc[t][beta]);
@@ -807,16 +823,11 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const Prefill
   // tile is past some row's causal limit (the tiles on the diagonal and the context end;
   // a wave-uniform branch around the mask only: one copy of the rest, whose registers a
   // second copy would double).
-  auto softmax = [&](int j, bool masked) __attribute__((always_inline)) {
+  // The first part of the softmax of tile j: the causal mask and each row's maximum
+  // (scaled to log2 units) into mx.
+  float mx[RT];
+  auto row_max = [&](int j, bool masked) __attribute__((always_inline)) {
     const int kt0 = j * KT;
-    // p = exp2(scale_log2 * s - m_run + kPLog2) (kPLog2 of the P.V type). The reference
-    // m_run is raised only when a score exceeds it by more than 2^8: a stale reference
-    // changes nothing in O / l (both carry the same factor), keeps p <= 2^(8 + kPLog2),
-    // and leaves O untouched on most tiles. The row tiles are independent chains: maxima
-    // first, one rescale branch, then every exp.
-    float mx[RT];
-    bool raise[RT];
-    bool any = false;
 #pragma unroll
     for (int t = 0; t < RT; ++t) {
       if (masked) {
@@ -833,6 +844,19 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const Prefill
 #pragma unroll
         for (int r = 0; r < 4; ++r) x = fmaxf(x, sc[t][beta][r]);
       mx[t] = score_rows_max(x) * a.scale_log2;
+    }
+  };
+  auto softmax = [&](int j, bool masked) __attribute__((always_inline)) {
+    // p = exp2(scale_log2 * s - m_run + kPLog2) (kPLog2 of the P.V type). The reference
+    // m_run is raised only when a score exceeds it by more than 2^8: a stale reference
+    // changes nothing in O / l (both carry the same factor), keeps p <= 2^(8 + kPLog2),
+    // and leaves O untouched on most tiles. The row tiles are independent chains: maxima
+    // first, one rescale branch, then every exp.
+    if (!PKV_PREFILL_EARLY_MAX) row_max(j, masked);
+    bool raise[RT];
+    bool any = false;
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
       raise[t] = mx[t] > m_run[t] + 8.f;  // also true the first time (m_run = -inf)
       any = any || raise[t];
     }
@@ -977,12 +1001,14 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a, const Prefill
   mfma_phase_begin();
   if (nt > 0) qk(0);
   mfma_phase_end();
+  if (PKV_PREFILL_EARLY_MAX && nt > 0) row_max(tbeg, tbeg >= j_mask);
   if (v_last >= 0) interval_v(0);
   for (int m = 1; m < nt; ++m) {
     open_m(m);
     mfma_phase_begin();
     pv_qk(m - 1, m);
     mfma_phase_end();
+    if (PKV_PREFILL_EARLY_MAX) row_max(tbeg + m, tbeg + m >= j_mask);
     interval_v(m);
   }
   for (int m = max(nt, 1); m <= ns; ++m) {
