@@ -415,6 +415,37 @@ def test_prefill_fp16_copy_scales_tiles_beyond_fp16():
         assert err <= ATOL * scale, (c, err, scale)
 
 
+def test_prefill_fp16_copy_at_the_widest_table():
+    """The fp16 copy at its widest table, 65,536 tokens: one chunk whose context is the
+    whole table, so its 256 region tiles' scale exponents fill the kernel's window of four
+    bytes per lane. The last tile holds values near 3e6 (a nonzero exponent in the
+    window's last byte), and its keys are query 0's head-0 vector doubled, so that
+    query attends almost only to that tile and a misread exponent would be off by 2^k.
+    Within 2e-3 of the oracle relative to the largest |V|; one block wider takes no
+    copy."""
+    _say("prefill fp16 copy widest table")
+    bs, nh, nkv, hd = 16, 4, 1, 64
+    n = 65536
+    spec = [(6, n)]
+    q, k, v, tables, ctx, cu = _chunks(spec, nh, nkv, hd, bs, torch.bfloat16, seed=23)
+    assert tables.shape[1] * bs == n
+    pos = torch.arange(n - 256, n)
+    big = tables[0, pos // bs].long() * bs + pos % bs
+    v[big] = (v[big].float() * 3e6).to(torch.bfloat16)
+    k[big, 0] = (q[0, 0].float() * 2).to(torch.bfloat16)
+    need = pa.prefill_workspace_bytes(torch.bfloat16, hd, nkv, 1, tables.shape[1], bs)
+    assert need > 0
+    assert pa.prefill_workspace_bytes(torch.bfloat16, hd, nkv, 1, tables.shape[1] + 1, bs) == 0
+    ws = torch.empty(need, dtype=torch.uint8, device=DEV)
+    ws.fill_(0xFF)
+    got = _prefill_c_abi("ws", q, k, v, tables, ctx, cu, bs, 6, ws)
+    want = oracle.prefill_attention(q, k, v, tables, cu, ctx, bs, threads=THREADS)
+    scale = v[big].float().abs().max().item()
+    assert torch.isfinite(got).all()
+    assert want[0, 0].abs().max().item() > 0.01 * scale  # query 0 reads the big tile
+    assert (got - want).abs().max().item() <= ATOL * scale
+
+
 @pytest.mark.parametrize("workspace", ["inside", "given"])
 def test_prefill_fp16_copy_under_graph_replay(workspace):
     """The two-dispatch bf16 prefill call (fp16 copy of V, then the matrix-core kernel)
