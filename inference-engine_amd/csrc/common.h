@@ -43,7 +43,7 @@ constexpr int kWave = 64;
 #define PKV_DECODE_COMBINE_CHUNK 4
 #endif
 #ifndef PKV_DECODE_COMBINE_SPLIT_PAIRS
-#define PKV_DECODE_COMBINE_SPLIT_PAIRS 2048
+#define PKV_DECODE_COMBINE_SPLIT_PAIRS 1024
 #endif
 // 1: the MFMA stream-K decode pass at head_dim 64 runs P.V on the matrix cores; 0: on
 // the VALU.
