@@ -51,10 +51,10 @@ constexpr int kWave = 64;
 #define PKV_DECODE_PV_MFMA 1
 #endif
 // One-launch cascade: the share of the unit stream each prefix workgroup takes after its
-// prefix items, in eighths of a stream workgroup's share (measured at config 3: 2 against
-// 0, 1, 3 and 4).
+// prefix items, in eighths of a stream workgroup's share (measured at config 3: 3 against
+// 1, 2, 4 and 5; 2 had been best before the prefix items got faster).
 #ifndef PKV_CASCADE_TAIL_EIGHTHS
-#define PKV_CASCADE_TAIL_EIGHTHS 2
+#define PKV_CASCADE_TAIL_EIGHTHS 3
 #endif
 #ifndef PKV_PREFILL_SWZ
 #define PKV_PREFILL_SWZ 1

@@ -441,7 +441,7 @@ int cascade_prefix_wg(int kv_dtype, int head_dim, int num_heads, int num_kv_head
   if (wg == 0) {
     // Measured on 256 CUs (prefix of 2,048 tokens, private tails of 0-1,024, 96-512
     // sequences): best with one item per prefix workgroup, plus one spare prefix
-    // workgroup per 32 resident ones (it only streams its quarter share) up to 56 items;
+    // workgroup per 32 resident ones (it only streams its tail share) up to 56 items;
     // past 80 items, two items each. The thresholds scale with the workgroups the GPU
     // holds at once (prefix workers are wg x ygrid).
     const int64_t slots = (int64_t)num_workgroups * p.ygrid;
