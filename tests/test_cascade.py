@@ -457,7 +457,7 @@ def _groups_batch(r, b, n_groups, bs, tail_max):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("seed", range(14))
+@pytest.mark.parametrize("seed", range(14 * max(1, int(os.environ.get("PKV_RANDOM_CASES_SCALE", "1")))))
 def test_cascade_random_shapes(seed):
     """Seeded random cascade steps: 65-600 sequences in 1-3 prefix groups (shared runs of
     4-40 blocks) plus private sequences, empty and short tails, head_dim 64/128, groups

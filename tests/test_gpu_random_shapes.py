@@ -3,7 +3,9 @@ ragged and empty contexts, block size (powers of two and not), head dim, GQA gro
 dtype and work split all drawn per case. Chunked prefill: chunk counts and lengths,
 cached prefixes, empty chunks, block sizes, head dims, groups and dtype (fp32 and
 head_dim 16 take the VALU kernel). Each case comes from
-its own seed and prints its shape first, so a failure names a reproducible case."""
+its own seed and prints its shape first, so a failure names a reproducible case.
+PKV_RANDOM_CASES_SCALE=N multiplies the number of seeds (here and in the cascade's
+random test)."""
 
 from __future__ import annotations
 
@@ -22,13 +24,15 @@ pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
 THREADS = min(16, os.cpu_count() or 1)
 ATOL = 2e-3
+# PKV_RANDOM_CASES_SCALE=N draws N times as many seeds per random test (default 1).
+SCALE = max(1, int(os.environ.get("PKV_RANDOM_CASES_SCALE", "1")))
 
 
 def _say(*a):
     print("[case]", *a, flush=True)
 
 
-@pytest.mark.parametrize("seed", range(32))
+@pytest.mark.parametrize("seed", range(32 * SCALE))
 def test_decode_random_shape(seed):
     r = random.Random(seed)
     hd = r.choice([16, 32, 64, 128, 128, 128, 256])
@@ -52,7 +56,7 @@ def test_decode_random_shape(seed):
     assert torch.equal(outq.cpu(), out32.cpu().to(dtype))
 
 
-@pytest.mark.parametrize("seed", range(12))
+@pytest.mark.parametrize("seed", range(12 * SCALE))
 def test_decode_random_large_batch(seed):
     """Batches past one wave (65 .. 1,100 sequences): the stream pass stages the batch's
     lengths, first columns and unit offsets in LDS up to 1,024 sequences and walks them
@@ -80,7 +84,7 @@ def test_decode_random_large_batch(seed):
     assert (out32.cpu() - want).abs().max().item() <= ATOL
 
 
-@pytest.mark.parametrize("seed", range(28))
+@pytest.mark.parametrize("seed", range(28 * SCALE))
 def test_prefill_random_shape(seed):
     r = random.Random(1000 + seed)
     hd = r.choice([16, 32, 64, 128, 128, 256])
