@@ -42,6 +42,12 @@ constexpr int kWave = 64;
 #ifndef PKV_DECODE_COMBINE_CHUNK
 #define PKV_DECODE_COMBINE_CHUNK 4
 #endif
+// Accumulator rows per load batch of the combine after a one-launch cascade, where
+// every (sequence, head) also folds a prefix part: 2 (measured at config 3: 110.5-110.9
+// against 111.1-111.3 µs with 4, 113.6 with 8).
+#ifndef PKV_CASCADE_COMBINE_CHUNK
+#define PKV_CASCADE_COMBINE_CHUNK 2
+#endif
 #ifndef PKV_DECODE_COMBINE_SPLIT_PAIRS
 #define PKV_DECODE_COMBINE_SPLIT_PAIRS 1024
 #endif

@@ -1256,7 +1256,7 @@ __global__ void __launch_bounds__(256)
 paged_decode_combine_kernel(const DecodeArgs a) {
   static_assert(SP == 1 || SP == 2, "one or two waves per (sequence, head)");
   constexpr int DPL = HD >= kWave ? HD / kWave : 1;  // head dims per lane
-  constexpr int kChunk = PKV_DECODE_COMBINE_CHUNK;    // accumulator rows per load batch
+  constexpr int kChunk = WT ? PKV_CASCADE_COMBINE_CHUNK : PKV_DECODE_COMBINE_CHUNK;  // rows per load batch
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int part = SP == 2 ? (wave & 1) : 0;  // which half of the records (SP = 2)
